@@ -1,0 +1,229 @@
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Primary line (``value``): large-batch paged decode at the Llama-3-8B head shape
+(Hq 32, Hkv 8, D 128, block_size 16, fp16 KV, 256 sequences, context ~ U[512,
+4096], shuffled block pool +10%), reported as achieved HBM GB/s over the
+algorithmic bytes (every attended K/V row once + q + out + table entries).
+
+The same JSON line also carries, under ``configs``, the other workloads of the
+benchmark set measured the same way: TinyLlama fp32 decode (latency), causal
+prefill fp16 L=512+1024 with the fused K/V write (TFLOP/s), long-context split
+decode bf16 16 x 32768 (GB/s).
+
+Timing: W warm-up launches, then K launches back to back bracketed by
+torch.cuda.synchronize() and HIP events on the stream the kernels run on
+(torch's current stream).  Small workloads are captured in a HIP graph of K
+launches so launch overhead is not measured.  ``cpu_baseline`` times the
+oracle's float32 restatement of the reference algorithm (padded gather, GQA
+expand, full scores, -1e9 mask, softmax, PV; llama.py:97-144) on the host for a
+bounded sample of the primary workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup, graph=False):
+    """Average ms per launch of ``fn`` over ``steps`` launches on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(steps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline_decode(wl, seconds=10.0, sample_seqs=16):
+    """Time the oracle's fp32 restatement of the reference on a sample of sequences."""
+    import torch
+    from oracle.attention import paged_decode_ref
+    idx = np.arange(min(sample_seqs, wl.batch))
+    bt = wl.block_tables[idx]
+    ctx = wl.context_lens[idx]
+    used = sorted(set(bt.reshape(-1).tolist()))
+    remap = {b: i for i, b in enumerate(used)}
+    bt_s = np.vectorize(remap.get)(bt).astype(np.int32)
+    sel = torch.tensor(used, dtype=torch.long, device=wl.k_cache.device)
+    kc = wl.k_cache.index_select(0, sel).float().cpu().numpy()
+    vc = wl.v_cache.index_select(0, sel).float().cpu().numpy()
+    q = wl.q[idx.tolist()].float().cpu().numpy()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        paged_decode_ref(q, kc, vc, bt_s, ctx, wl.num_heads, wl.num_kv_heads, wl.head_dim, wl.block_size,
+                         acc=np.float32)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    es = wl.k_cache.element_size()
+    b = len(idx)
+    blocks = int(((ctx.astype(np.int64) + wl.block_size - 1) // wl.block_size).sum())
+    sample_bytes = (int(ctx.astype(np.int64).sum()) * wl.num_kv_heads * wl.head_dim * 2 * es
+                    + b * wl.num_heads * wl.head_dim * 2 * es + blocks * 4 + b * 4)
+    threads = torch.get_num_threads()
+    return {
+        "value": round(sample_bytes * n / el / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{b} of {wl.batch} sequences (sum ctx {int(ctx.sum())}), {n} passes in {el:.1f} s; "
+                   f"numpy float32 restatement of llama.py:97-144 incl. padded gather to the {bt.shape[1]}-block "
+                   f"table width; host cpus {len(os.sched_getaffinity(0))} of {os.cpu_count()}"),
+        "ms_per_call": round(el / n * 1e3, 3),
+    }
+
+
+def bench_decode(wl, steps, warmup, graph):
+    from tinyvllm_amd.attention import PagedDecodePlan
+    plan = PagedDecodePlan(wl.q, wl.k_cache, wl.v_cache, wl.bt_dev, wl.ctx_dev, wl.num_heads,
+                           wl.num_kv_heads, wl.head_dim, wl.block_size)
+    ms = timed(plan.run, steps, warmup, graph)
+    gbs = wl.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    return {"ms": ms, "gbs": gbs, "bytes": wl.algorithmic_bytes(), "flops": wl.flops(),
+            "partition_size": plan.partition_size}
+
+
+def bench_prefill(steps, warmup):
+    import torch
+    from tinyvllm_amd.attention import PrefillPlan
+    from tinyvllm_amd.kv_cache import reshape_and_cache
+    from tinyvllm_amd.workloads import config2_prefill_tinyllama
+    wl = config2_prefill_tinyllama()
+    plans = [PrefillPlan(q, k, v, True) for q, k, v in zip(wl.q, wl.k, wl.v)]
+    per = [timed(p.run, steps, warmup, graph=True) for p in plans]
+    kc = torch.zeros((wl.num_blocks, 16, 4, 64), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+
+    def write():
+        for k, v, s in zip(wl.k, wl.v, wl.slots_dev):
+            reshape_and_cache(kc, vc, k[0], v[0], s)
+    wms = timed(write, steps, warmup, graph=True)
+    tot = sum(per)
+    flops = wl.flops()
+    return {
+        "workload": "prefill_tinyllama_f16_L512+L1024 (Hq32 Hkv4 D64, causal) + fused KV write",
+        "value": round(flops / (tot * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+        "ms_per_prompt": [round(x, 5) for x in per],
+        "flops": flops,
+        "frac_of_fp16_mfma_peak": round(flops / (tot * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+        "kv_write_ms": round(wms, 5),
+        "kv_write_gbs": round(wl.kv_write_bytes() / (wms * 1e-3) / 1e9, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--primary-only", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
+                 "(the attention hot path shards by sequence or KV head with no exchange; see DESIGN.md)")
+
+    import torch
+    from tinyvllm_amd import workloads
+
+    torch.cuda.set_device(0)
+    log("bench: config3 decode (B256 Hq32 Hkv8 D128 fp16)")
+    wl3 = workloads.config3_decode_llama3_8b()
+    torch.cuda.synchronize()
+    r3 = bench_decode(wl3, args.steps, args.warmup, graph=False)
+    log(f"bench: config3 {r3['ms']:.4f} ms {r3['gbs']:.1f} GB/s")
+
+    configs = {}
+    if not args.primary_only:
+        log("bench: config1 decode (TinyLlama fp32)")
+        wl1 = workloads.config1_decode_tinyllama()
+        r1 = bench_decode(wl1, args.steps, args.warmup, graph=True)
+        configs["decode_tinyllama_f32_b4"] = {
+            "value": round(r1["ms"] * 1e3, 3), "unit": "us", "gbs": round(r1["gbs"], 1),
+            "bytes": r1["bytes"], "note": "cache-resident (~1 MB): latency-bound, not an HBM figure"}
+        del wl1
+        log("bench: config2 prefill")
+        configs["prefill_tinyllama_f16"] = bench_prefill(args.steps, args.warmup)
+        log("bench: config5 long split decode (B16 x 32768 bf16)")
+        wl5 = workloads.config5_decode_long()
+        r5 = bench_decode(wl5, max(10, args.steps // 2), args.warmup, graph=False)
+        configs["decode_long_bf16_b16_32k"] = {
+            "value": round(r5["gbs"], 1), "unit": "GB/s", "ms": round(r5["ms"], 4),
+            "frac_of_hbm_peak": round(r5["gbs"] / HBM_PEAK_GBS, 4), "bytes": r5["bytes"],
+            "partition_size": r5["partition_size"]}
+        del wl5
+        configs["e2e_tinyllama_decode"] = {"value": None, "unit": "tok/s", "note": "not built yet"}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline (oracle float32 restatement)")
+        cpu = cpu_baseline_decode(wl3, seconds=args.cpu_seconds)
+
+    line = {
+        "metric": "paged-decode HBM GB/s (% of peak), prefill TFLOP/s, TinyLlama decode tok/s",
+        "value": round(r3["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r3["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) q/k/v; seeded context lengths and shuffled block tables)",
+        "config": {"workload": "paged_decode Llama-3-8B head shape: B256 Hq32 Hkv8 D128 block16 fp16 KV, "
+                               "ctx~U[512,4096] seed 0, pool +10% shuffled",
+                   "sum_ctx": int(wl3.context_lens.astype(np.int64).sum()),
+                   "partition_size": r3["partition_size"]},
+        "roofline": {"bound": "hbm", "achieved": round(r3["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r3["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": r3["bytes"],
+                     "timing": "HIP events over K launches of decode+merge on the launch stream"},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,87 @@
+"""The C ABI: libtvattn.so loads on the host and exports exactly what include/tv_attn.h declares.
+
+Only host-side entry points run here (no kernel launch): argument validation
+paths return before any HIP call.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tinyvllm_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tv_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(tv_[a-z_0-9]+)\s*\(", text, flags=re.M))
+
+
+def test_header_parses():
+    names = declared_functions()
+    assert {"tv_paged_decode", "tv_flash_prefill", "tv_reshape_and_cache", "tv_write_kv",
+            "tv_read_kv_blocks", "tv_last_error", "tv_abi_version",
+            "tv_paged_decode_workspace_bytes"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in tv_attn.h but not exported"
+    assert set(_lib.SIGNATURES) == declared_functions()
+    assert lib.tv_abi_version() == _lib.ABI_VERSION
+
+
+def test_argument_counts_match_header():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), name
+
+
+def test_workspace_size_is_host_arithmetic():
+    lib = _lib.load()
+    assert lib.tv_paged_decode_workspace_bytes(4, 32, 64, 16, 16, 512) == 0      # one partition
+    # 256 seqs x 32 heads x 8 partitions x (128 + 2) floats
+    assert lib.tv_paged_decode_workspace_bytes(256, 32, 128, 256, 16, 512) == 256 * 32 * 8 * 130 * 4
+
+
+def test_validation_errors_are_reported_without_launch():
+    lib = _lib.load()
+    rc = lib.tv_paged_decode(None, None, None, None, None, None, 1, 32, 8, 128, 16, 10, 4, 4,
+                             0.1, 1, 1, 512, None, 0, None)
+    assert rc == _lib.TV_EINVAL
+    assert b"null pointer" in lib.tv_last_error()
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.check(rc, "tv_paged_decode")
+    fake = ctypes.c_void_p(16)      # never dereferenced: rejected before any launch
+    rc = lib.tv_paged_decode(fake, fake, fake, fake, fake, fake, 1, 32, 8, 96, 16, 10, 4, 4,
+                             0.1, 1, 1, 512, None, 0, None)
+    assert rc == _lib.TV_EUNSUPPORTED and b"head_dim 96" in lib.tv_last_error()
+    rc = lib.tv_paged_decode(fake, fake, fake, fake, fake, fake, 1, 32, 8, 128, 16, 10, 4, 4,
+                             0.1, 1, 1, 500, None, 0, None)
+    assert rc == _lib.TV_EINVAL and b"partition_size" in lib.tv_last_error()
+    rc = lib.tv_paged_decode(fake, fake, fake, fake, fake, fake, 1, 32, 8, 128, 16, 10, 64, 64,
+                             0.1, 1, 1, 512, None, 0, None)
+    assert rc == _lib.TV_EINVAL and b"workspace" in lib.tv_last_error()
+    rc = lib.tv_write_kv(fake, fake, fake, fake, 10, 0, 1, 4, 64, 16, 10, 256, 256, 1, None)
+    assert rc == _lib.TV_EINVAL and b"block_id" in lib.tv_last_error()
+    rc = lib.tv_write_kv(fake, fake, fake, fake, 0, 10, 7, 4, 64, 16, 10, 256, 256, 1, None)
+    assert rc == _lib.TV_EINVAL and b"do not fit" in lib.tv_last_error()
+    rc = lib.tv_flash_prefill(fake, fake, fake, fake, 0, 4, 8, 8, 64, 64, 512, 512, 512, 512,
+                              1, 0.1, 1, 1, None)
+    assert rc == _lib.TV_EINVAL and b"empty" in lib.tv_last_error()
+    rc = lib.tv_read_kv_blocks(fake, fake, fake, fake, fake, 1, 17, 4, 64, 16, 10, 1, None)
+    assert rc == _lib.TV_EINVAL and b"exceeds" in lib.tv_last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(ImportError, match="no fallback"):
+        _lib.load()

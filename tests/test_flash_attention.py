@@ -1,0 +1,145 @@
+"""Prefill attention on the GPU vs the oracle (tinyvllm/model/llama.py:58-94).
+
+Restates tests/test_flash_attention.py of the reference (shapes, GQA, causal
+known answers, sequence lengths, head dims, dtypes, TinyLlama shapes) and adds
+MFMA-path parity for fp16/bf16 at the benchmark shapes.
+Tolerances (max-abs vs the float64 oracle): fp32 1e-4, fp16/bf16 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import flash_prefill_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def _op():
+    from tinyvllm_amd.attention import flash_prefill_attention
+    return flash_prefill_attention
+
+
+def flash(q, k, v, causal=True):
+    """[L, H, D] wrapper like the reference test's (adds and removes the batch dim)."""
+    out = _op()(q.unsqueeze(0).cuda(), k.unsqueeze(0).cuda(), v.unsqueeze(0).cuda(), causal)
+    torch.cuda.synchronize()
+    return out.squeeze(0)
+
+
+def randn(seed, *shape, dtype=torch.float32):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(dtype)
+
+
+def check(q, k, v, causal=True, tol=None):
+    out = flash(q, k, v, causal)
+    want = flash_prefill_ref(q.float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None], causal)[0]
+    err = np.abs(out.float().cpu().numpy() - want).max()
+    tol = TOL[q.dtype] if tol is None else tol
+    assert err <= tol, f"max-abs {err} > {tol}"
+    return out
+
+
+# ---- restated reference tests ------------------------------------------------------
+
+def test_output_shape():
+    out = flash(randn(0, 16, 8, 64), randn(1, 16, 8, 64), randn(2, 16, 8, 64))
+    assert out.shape == (16, 8, 64)
+
+
+@pytest.mark.parametrize("lq,hq,hkv,d", [(32, 4, 4, 32), (32, 32, 8, 64), (16, 8, 4, 32), (16, 32, 8, 64),
+                                          (16, 32, 4, 64), (64, 32, 8, 64), (256, 32, 8, 64)])
+def test_matches_standard_attention(lq, hq, hkv, d):
+    check(randn(3, lq, hq, d), randn(4, lq, hkv, d), randn(5, lq, hkv, d))
+
+
+def test_non_causal():
+    check(randn(6, 16, 4, 32), randn(7, 16, 4, 32), randn(8, 16, 4, 32), causal=False)
+
+
+def test_causal_mask_first_token():
+    q = torch.zeros(8, 2, 16)
+    q[0] = 1.0
+    k = randn(9, 8, 2, 16)
+    v = torch.eye(8).unsqueeze(1).expand(8, 2, 8).contiguous()     # head_dim_v 8 != head_dim 16
+    out = check(q, k, v)
+    assert out[0, 0, 0].item() > 0.5
+
+
+def test_last_token_attends_to_all():
+    q = torch.ones(8, 2, 16)
+    k = torch.zeros(8, 2, 16)
+    v = torch.arange(8).reshape(8, 1, 1).expand(8, 2, 16).float().contiguous()
+    out = flash(q, k, v)
+    assert abs(out[-1, 0, 0].item() - 3.5) < 1e-2
+
+
+@pytest.mark.parametrize("q_len", [1, 2, 7, 8, 15, 16, 31, 32, 63, 64, 128])
+def test_various_lengths(q_len):
+    check(randn(10, q_len, 4, 32), randn(11, q_len, 4, 32), randn(12, q_len, 4, 32))
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_various_head_dims(head_dim):
+    check(randn(13, 16, 4, head_dim), randn(14, 16, 4, head_dim), randn(15, 16, 4, head_dim))
+
+
+def test_float16_finite():
+    q, k, v = (randn(16 + i, 32, 4, 32, dtype=torch.float16) for i in range(3))
+    out = check(q, k, v)
+    assert out.shape == (32, 4, 32) and torch.isfinite(out).all()
+
+
+def test_float32_dtype():
+    out = flash(randn(19, 32, 4, 32), randn(20, 32, 4, 32), randn(21, 32, 4, 32))
+    assert out.dtype == torch.float32 and out.shape == (32, 4, 32)
+
+
+# ---- MFMA path (fp16 / bf16, head_dim 64 / 128) --------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("lq", [1, 15, 64, 65, 200])
+@pytest.mark.parametrize("causal", [True, False])
+def test_mfma_path(dtype, d, lq, causal):
+    hq, hkv = 8, 2
+    check(randn(22, lq, hq, d, dtype=dtype), randn(23, lq, hkv, d, dtype=dtype),
+          randn(24, lq, hkv, d, dtype=dtype), causal)
+
+
+@pytest.mark.parametrize("length", [512, 1024])
+def test_tinyllama_prefill_config2(length):
+    """Config 2 shape: Hq 32, Hkv 4, D 64, fp16 inputs, causal."""
+    q, k, v = (randn(30 + i, length, 32 if i == 0 else 4, 64, dtype=torch.float16) for i in range(3))
+    check(q, k, v)
+
+
+def test_unequal_lengths_top_left_causal():
+    q = randn(40, 40, 8, 64, dtype=torch.float16)
+    k = randn(41, 100, 2, 64, dtype=torch.float16)
+    v = randn(42, 100, 2, 64, dtype=torch.float16)
+    check(q, k, v, True)
+    q32 = randn(43, 10, 4, 32)
+    check(q32, randn(44, 30, 4, 32), randn(45, 30, 4, 32), True)
+
+
+def test_strided_inputs_from_fused_qkv():
+    """q/k/v as views into one [L, (Hq+2Hkv)*D] projection output."""
+    L, hq, hkv, d = 96, 8, 2, 64
+    qkv = randn(46, L, (hq + 2 * hkv) * d, dtype=torch.float16).cuda()
+    q = qkv[:, :hq * d].view(L, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(L, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(L, hkv, d)
+    out = _op()(q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), True)[0]
+    want = flash_prefill_ref(q.float().cpu().numpy()[None], k.float().cpu().numpy()[None],
+                             v.float().cpu().numpy()[None], True)[0]
+    assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-2
+
+
+def test_rejects_batch_above_one():
+    q = randn(47, 2, 8, 4, 32).cuda()
+    with pytest.raises(ValueError, match="batch 1"):
+        _op()(q, q[:, :, :4], q[:, :, :4], True)

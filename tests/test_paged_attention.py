@@ -1,0 +1,179 @@
+"""Paged decode attention on the GPU vs the oracle (tinyvllm/model/llama.py:97-144).
+
+Restates tests/test_paged_attention.py of the reference (consecutive-block
+fixture, GQA 4x/8x, batching, context lengths, non-multiple context) and adds
+parity on shuffled pools for every supported dtype / head_dim / group size,
+the split-context path, and the reference's edge semantics.
+Tolerances (max-abs vs the float64 oracle): fp32 1e-4, fp16/bf16 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import paged_decode_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def _ops():
+    from tinyvllm_amd.attention import paged_decode_attention
+    return paged_decode_attention
+
+
+def build_case(seed, ctx_list, hq, hkv, d, bs, dtype, spare=5, shuffle=True, width=None):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    need = [(max(c, 1) + bs - 1) // bs for c in ctx_list]
+    nb = sum(need) + spare
+    ids = rng.permutation(nb) if shuffle else np.arange(nb)
+    mb = max(need) if width is None else width
+    bt = np.zeros((len(ctx_list), mb), np.int32)
+    cur = 0
+    for i, n in enumerate(need):
+        bt[i, :min(n, mb)] = ids[cur:cur + n][:mb]
+        cur += n
+    q = torch.from_numpy(rng.standard_normal((len(ctx_list), 1, hq, d), dtype=np.float32)).to(dtype)
+    kc = torch.from_numpy(rng.standard_normal((nb, bs, hkv, d), dtype=np.float32)).to(dtype)
+    vc = torch.from_numpy(rng.standard_normal((nb, bs, hkv, d), dtype=np.float32)).to(dtype)
+    return q, kc, vc, bt, np.asarray(ctx_list, np.int32)
+
+
+def run(q, kc, vc, bt, cl, hq, hkv, d, bs, **kw):
+    dev = "cuda"
+    out = _ops()(q.to(dev), kc.to(dev), vc.to(dev), torch.from_numpy(bt).to(dev),
+                 torch.from_numpy(cl).to(dev), hq, hkv, d, bs, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle(q, kc, vc, bt, cl, hq, hkv, d, bs, **kw):
+    return paged_decode_ref(q.float().numpy(), kc.float().numpy(), vc.float().numpy(), bt, cl,
+                            hq, hkv, d, bs, **kw)
+
+
+def check(case, hq, hkv, d, bs, dtype, **kw):
+    q, kc, vc, bt, cl = case
+    got = run(q, kc, vc, bt, cl, hq, hkv, d, bs, **kw)
+    assert got.shape == (len(cl), 1, hq, d) and got.dtype == dtype
+    okw = {k: v for k, v in kw.items() if k == "max_context_len"}
+    want = oracle(q, kc, vc, bt, cl, hq, hkv, d, bs, **okw)
+    err = np.abs(got.float().cpu().numpy() - want).max()
+    assert err <= TOL[dtype], f"max-abs {err} > {TOL[dtype]}"
+    return got
+
+
+# ---- restated reference tests (consecutive blocks, fp32) ---------------------------
+
+@pytest.mark.parametrize("batch,hq,hkv,d,ctx", [
+    (2, 8, 8, 64, 32),      # test_output_shape
+    (1, 4, 4, 32, 32),      # test_matches_standard_attention
+    (1, 32, 8, 64, 32),     # test_gqa_4x
+    (1, 32, 4, 64, 64),     # test_gqa_8x (TinyLlama)
+    (4, 8, 8, 32, 32),      # test_batch_size_4
+    (1, 4, 4, 32, 16), (1, 4, 4, 32, 64), (1, 4, 4, 32, 128),   # test_various_context_lengths
+])
+def test_reference_cases(batch, hq, hkv, d, ctx):
+    case = build_case(1, [ctx] * batch, hq, hkv, d, 16, torch.float32, shuffle=False)
+    check(case, hq, hkv, d, 16, torch.float32)
+
+
+def test_context_not_multiple_of_block_size():
+    case = build_case(2, [25], 4, 4, 32, 16, torch.float32, shuffle=False)
+    out = check(case, 4, 4, 32, 16, torch.float32)
+    assert not torch.isnan(out).any() and not torch.isinf(out).any()
+
+
+# ---- parity on shuffled pools ------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
+def test_head_dims_and_dtypes(dtype, d):
+    case = build_case(3, [1, 17, 100, 250], 8, 2, d, 16, dtype)
+    check(case, 8, 2, d, 16, dtype)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4), (16, 4), (32, 4), (32, 2), (24, 8), (12, 2), (6, 1)])
+def test_group_sizes(hq, hkv):
+    case = build_case(4, [5, 40, 77], hq, hkv, 64, 16, torch.float16)
+    check(case, hq, hkv, 64, 16, torch.float16)
+
+
+@pytest.mark.parametrize("bs", [1, 4, 8, 12, 32])
+def test_block_sizes(bs):
+    case = build_case(5, [3, 31, 65], 8, 2, 64, bs, torch.float32)
+    check(case, 8, 2, 64, bs, torch.float32)
+
+
+@pytest.mark.parametrize("psize", [16, 48, 64, 512, 4096])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_split_context_partitions(psize, dtype):
+    case = build_case(6, [1, 15, 16, 17, 300, 1000], 16, 4, 128, 16, dtype)
+    check(case, 16, 4, 128, 16, dtype, partition_size=psize)
+
+
+def test_tinyllama_config1_workload():
+    """Config 1: TinyLlama layer, fp32, ctx {17,64,128,250}, shuffled 64-block pool."""
+    from tinyvllm_amd.workloads import config1_decode_tinyllama
+    wl = config1_decode_tinyllama(device="cuda")
+    out = _ops()(wl.q, wl.k_cache, wl.v_cache, wl.bt_dev, wl.ctx_dev, 32, 4, 64, 16)
+    want = paged_decode_ref(wl.host["q"], wl.host["k_cache"], wl.host["v_cache"], wl.block_tables,
+                            wl.context_lens, 32, 4, 64, 16)
+    assert np.abs(out.cpu().numpy() - want).max() <= 1e-4
+
+
+# ---- reference edge semantics --------------------------------------------------------
+
+def test_max_context_len_trims_table():
+    case = build_case(7, [20, 64], 8, 4, 64, 16, torch.float32, width=8)
+    check(case, 8, 4, 64, 16, torch.float32, max_context_len=40)
+
+
+def test_context_beyond_table_is_truncated():
+    q, kc, vc, bt, cl = build_case(8, [30, 64], 8, 4, 64, 16, torch.float32)
+    cl = np.array([30, 1000], np.int32)           # seq 1 claims more than its 4 blocks
+    check((q, kc, vc, bt, cl), 8, 4, 64, 16, torch.float32)
+
+
+def test_context_zero_reproduces_reference_mean():
+    q, kc, vc, bt, cl = build_case(9, [20, 33], 8, 2, 64, 16, torch.float32)
+    q = q * 0.05
+    cl = np.array([0, 33], np.int32)
+    check((q, kc, vc, bt, cl), 8, 2, 64, 16, torch.float32)
+
+
+def test_invalid_block_id_gives_nan_not_fault():
+    q, kc, vc, bt, cl = build_case(10, [20, 33], 8, 2, 64, 16, torch.float32)
+    bt = bt.copy()
+    bt[1, 1] = kc.shape[0] + 1000                 # outside the cache
+    out = run(q, kc, vc, bt, cl, 8, 2, 64, 16).cpu().numpy()
+    assert np.isnan(out[1]).all()
+    want = oracle(q, kc, vc, bt[:1], cl[:1], 8, 2, 64, 16)
+    assert np.abs(out[:1] - want).max() <= 1e-4
+
+
+def test_deterministic():
+    case = build_case(11, [100, 700, 3], 32, 8, 128, 16, torch.float16)
+    a = run(*case, 32, 8, 128, 16, partition_size=128)
+    b = run(*case, 32, 8, 128, 16, partition_size=128)
+    assert torch.equal(a, b)
+
+
+def test_fp32_output_for_half_inputs():
+    case = build_case(12, [50, 9], 8, 8, 64, 16, torch.float16)
+    q, kc, vc, bt, cl = case
+    out = run(q, kc, vc, bt, cl, 8, 8, 64, 16, out_dtype=torch.float32)
+    assert out.dtype == torch.float32
+    assert np.abs(out.cpu().numpy() - oracle(*case, 8, 8, 64, 16)).max() <= 2e-2
+
+
+def test_rejects_bad_arguments():
+    q, kc, vc, bt, cl = build_case(13, [10], 8, 2, 64, 16, torch.float32)
+    dev = "cuda"
+    with pytest.raises(ValueError):
+        _ops()(q.to(dev), kc.to(dev), vc.to(dev), torch.from_numpy(bt).long().to(dev),
+               torch.from_numpy(cl).to(dev), 8, 2, 64, 16)
+    with pytest.raises(ValueError):
+        _ops()(q.to(dev), kc.to(dev), vc.to(dev), torch.from_numpy(bt).to(dev),
+               torch.from_numpy(cl).to(dev), 8, 4, 64, 16)

@@ -1,0 +1,201 @@
+"""Drop-in attention entry points with the reference's signatures.
+
+``paged_decode_attention`` and ``flash_prefill_attention`` keep the names,
+positional order and keyword names of tinyvllm/model/llama.py:97-108 and
+llama.py:58-63, so callers written against the reference (the JIT decode body,
+Attention.__call__, the tests) can switch by import.  Tensors are PyTorch-ROCm
+tensors on a HIP device; all arithmetic runs in libtvattn.so (no fallback).
+"""
+
+import math
+
+import torch
+
+from . import _lib
+
+_lib.load()
+
+DEFAULT_PARTITION = 512
+
+
+def _require(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _on_gpu(*tensors):
+    dev = tensors[0].device
+    _require(dev.type == "cuda", f"tensors must live on a HIP device (got {dev})")
+    for t in tensors:
+        _require(t.device == dev, "all tensors must be on the same device")
+    return dev
+
+
+def default_partition_size(num_seqs, num_kv_heads, width, num_cus=256):
+    """Tokens per decode work-group.
+
+    Sequences longer than one partition are split across work-groups and merged
+    by a second kernel.  512 keeps >= 2 partitions per CU for long contexts while
+    the merge traffic stays < 1% of the K/V bytes; short batches with few
+    (sequence, KV head) pairs use smaller partitions to fill the CUs.
+    """
+    pairs = max(1, num_seqs * num_kv_heads)
+    p = DEFAULT_PARTITION
+    while p > 64 and pairs * ((width + p - 1) // p) < 2 * num_cus:
+        p //= 2
+    return p
+
+
+def paged_decode_attention(queries, k_cache, v_cache, block_tables, context_lens,
+                           n_heads, n_kv_heads, head_dim, block_size, max_context_len=None,
+                           *, partition_size=None, out_dtype=None):
+    """Paged decode attention (tinyvllm/model/llama.py:97-144).
+
+    queries [B,1,Hq,D]; k_cache/v_cache [NB,bs,Hkv,D] (same dtype as queries);
+    block_tables [B,MB] int32 zero-padded; context_lens [B] int32.
+    Returns [B,1,Hq,D] in ``out_dtype`` (default: the query dtype).
+    ``max_context_len`` trims the table to ceil(max_context_len/bs) columns as in
+    the reference.  ``partition_size`` (keyword-only, not in the reference)
+    forces the split-context partition length in tokens.
+    """
+    lib = _lib.load()
+    dev = _on_gpu(queries, k_cache, v_cache, block_tables, context_lens)
+    _require(queries.dim() == 4 and queries.shape[1] == 1, f"queries must be [B,1,Hq,D], got {tuple(queries.shape)}")
+    b, _, hq, d = queries.shape
+    _require(hq == n_heads and d == head_dim, "queries shape does not match n_heads/head_dim")
+    nb, bs, hkv, d2 = k_cache.shape
+    _require(tuple(v_cache.shape) == (nb, bs, hkv, d2), "k_cache and v_cache shapes differ")
+    _require(bs == block_size and hkv == n_kv_heads and d2 == head_dim,
+             f"cache shape {tuple(k_cache.shape)} does not match block_size/n_kv_heads/head_dim")
+    _require(n_heads % n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads")
+    _require(queries.dtype == k_cache.dtype == v_cache.dtype, "queries and caches must share a dtype")
+    _require(block_tables.dtype == torch.int32 and context_lens.dtype == torch.int32,
+             "block_tables and context_lens must be int32")
+    _require(block_tables.dim() == 2 and block_tables.shape[0] == b, "block_tables must be [B, max_blocks]")
+    _require(context_lens.numel() == b, "context_lens must have B entries")
+    for t in (queries, k_cache, v_cache, block_tables, context_lens):
+        _require(t.is_contiguous(), "all inputs must be contiguous")
+
+    mb = block_tables.shape[1]
+    used = mb
+    if max_context_len is not None:
+        used = min((int(max_context_len) + block_size - 1) // block_size, mb)
+    _require(used > 0, "no block table columns to attend over")
+    width = used * block_size
+    if partition_size is None:
+        partition_size = default_partition_size(b, n_kv_heads, width)
+    out_dtype = queries.dtype if out_dtype is None else out_dtype
+    out = torch.empty((b, 1, hq, d), dtype=out_dtype, device=dev)
+    ws_bytes = lib.tv_paged_decode_workspace_bytes(b, hq, d, used, block_size, partition_size)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.tv_paged_decode(
+        out.data_ptr(), queries.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_tables.data_ptr(), context_lens.data_ptr(),
+        b, hq, n_kv_heads, d, block_size, nb, mb, used,
+        1.0 / math.sqrt(head_dim), _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype),
+        int(partition_size), ws.data_ptr() if ws is not None else None, ws_bytes,
+        _lib.stream_ptr(dev))
+    _lib.check(rc, "paged_decode_attention")
+    return out
+
+
+def _token_rows(t, name):
+    """[1, L, H, D] tensor whose (H, D) rows are dense; returns the token stride."""
+    _require(t.dim() == 4 and t.shape[0] == 1, f"{name} must be [1, L, H, D] (batch 1, llama.py:65-67)")
+    _require(t.stride(3) == 1 and t.stride(2) == t.shape[3], f"{name}: heads and head_dim must be contiguous")
+    return t.stride(1)
+
+
+def flash_prefill_attention(queries, keys, values, causal=True, *, out_dtype=None):
+    """Prefill attention over one prompt (tinyvllm/model/llama.py:58-94).
+
+    queries [1,Lq,Hq,D], keys [1,Lk,Hkv,D], values [1,Lk,Hkv,Dv] -> [1,Lq,Hq,Dv].
+    ``causal`` masks key j for query i when j > i (top-left aligned).
+    """
+    lib = _lib.load()
+    dev = _on_gpu(queries, keys, values)
+    qs = _token_rows(queries, "queries")
+    ks = _token_rows(keys, "keys")
+    vs = _token_rows(values, "values")
+    _, lq, hq, d = queries.shape
+    _, lk, hkv, dk = keys.shape
+    _require(dk == d, "queries and keys must share head_dim")
+    _require(values.shape[1] == lk and values.shape[2] == hkv, "keys and values must share [L, Hkv]")
+    _require(hq % hkv == 0, "query heads must be a multiple of KV heads")
+    _require(queries.dtype == keys.dtype == values.dtype, "queries, keys and values must share a dtype")
+    dv = values.shape[3]
+    out_dtype = queries.dtype if out_dtype is None else out_dtype
+    out = torch.empty((1, lq, hq, dv), dtype=out_dtype, device=dev)
+    rc = lib.tv_flash_prefill(
+        out.data_ptr(), queries.data_ptr(), keys.data_ptr(), values.data_ptr(),
+        lq, lk, hq, hkv, d, dv, qs, ks, vs, hq * dv, 1 if causal else 0,
+        1.0 / math.sqrt(d), _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype),
+        _lib.stream_ptr(dev))
+    _lib.check(rc, "flash_prefill_attention")
+    return out
+
+
+class PagedDecodePlan:
+    """Pre-validated, pointer-stable paged decode for a fixed batch shape.
+
+    Holds the output and split-context workspace so that ``run()`` is a single
+    C call with no allocation -- the form a decode loop captures in a HIP graph
+    (the analogue of the reference's TinyJit replay, llama.py:290-344).  The
+    input tensors must stay alive and keep their storage while the plan is used.
+    """
+
+    def __init__(self, queries, k_cache, v_cache, block_tables, context_lens,
+                 n_heads, n_kv_heads, head_dim, block_size, max_context_len=None,
+                 *, partition_size=None, out_dtype=None):
+        self.lib = _lib.load()
+        self.dev = _on_gpu(queries, k_cache, v_cache, block_tables, context_lens)
+        b = queries.shape[0]
+        mb = block_tables.shape[1]
+        used = mb if max_context_len is None else min((int(max_context_len) + block_size - 1) // block_size, mb)
+        _require(used > 0, "no block table columns to attend over")
+        if partition_size is None:
+            partition_size = default_partition_size(b, n_kv_heads, used * block_size)
+        self.partition_size = int(partition_size)
+        out_dtype = queries.dtype if out_dtype is None else out_dtype
+        # validate once through the functional path's checks
+        _require(queries.shape == (b, 1, n_heads, head_dim), "queries must be [B,1,Hq,D]")
+        _require(tuple(k_cache.shape[1:]) == (block_size, n_kv_heads, head_dim), "cache shape mismatch")
+        _require(block_tables.dtype == torch.int32 and context_lens.dtype == torch.int32, "int32 tables required")
+        for t in (queries, k_cache, v_cache, block_tables, context_lens):
+            _require(t.is_contiguous(), "all inputs must be contiguous")
+        self.out = torch.empty((b, 1, n_heads, head_dim), dtype=out_dtype, device=self.dev)
+        self.ws_bytes = self.lib.tv_paged_decode_workspace_bytes(b, n_heads, head_dim, used, block_size,
+                                                                 self.partition_size)
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=self.dev)
+        self._inputs = (queries, k_cache, v_cache, block_tables, context_lens)
+        self.args = (self.out.data_ptr(), queries.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                     block_tables.data_ptr(), context_lens.data_ptr(), b, n_heads, n_kv_heads, head_dim,
+                     block_size, k_cache.shape[0], mb, used, 1.0 / math.sqrt(head_dim),
+                     _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), self.partition_size,
+                     self.ws.data_ptr(), self.ws_bytes)
+
+    def run(self):
+        _lib.check(self.lib.tv_paged_decode(*self.args, _lib.stream_ptr(self.dev)), "PagedDecodePlan.run")
+        return self.out
+
+
+class PrefillPlan:
+    """Pre-validated, pointer-stable causal prefill for fixed [1, L, H, D] inputs."""
+
+    def __init__(self, queries, keys, values, causal=True, *, out_dtype=None):
+        self.lib = _lib.load()
+        self.dev = _on_gpu(queries, keys, values)
+        qs, ks, vs = _token_rows(queries, "queries"), _token_rows(keys, "keys"), _token_rows(values, "values")
+        _, lq, hq, d = queries.shape
+        _, lk, hkv, _ = keys.shape
+        dv = values.shape[3]
+        out_dtype = queries.dtype if out_dtype is None else out_dtype
+        self.out = torch.empty((1, lq, hq, dv), dtype=out_dtype, device=self.dev)
+        self._inputs = (queries, keys, values)
+        self.args = (self.out.data_ptr(), queries.data_ptr(), keys.data_ptr(), values.data_ptr(),
+                     lq, lk, hq, hkv, d, dv, qs, ks, vs, hq * dv, 1 if causal else 0, 1.0 / math.sqrt(d),
+                     _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype))
+
+    def run(self):
+        _lib.check(self.lib.tv_flash_prefill(*self.args, _lib.stream_ptr(self.dev)), "PrefillPlan.run")
+        return self.out

@@ -1,0 +1,281 @@
+// extern "C" entry points of libtvattn.so (declared in include/tv_attn.h).
+// Host-side validation lives here; kernels assume validated arguments.
+#include <cstdio>
+#include <cstdarg>
+#include <initializer_list>
+#include <string>
+
+#include "../../include/tv_attn.h"
+#include "paged_decode_inst.h"
+#include "tv_params.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return TV_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TV_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool valid_dtype(int d) { return d == TV_F32 || d == TV_F16 || d == TV_BF16; }
+int elem_size(int d) { return d == TV_F32 ? 4 : 2; }
+bool pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
+int ilog2(long long x) {
+  int r = 0;
+  while ((1LL << r) < x) ++r;
+  return r;
+}
+
+// Largest power of two <= 8 that divides the GQA group.
+int heads_per_group_chunk(int group) {
+  for (int gt = 8; gt > 1; gt >>= 1)
+    if (group % gt == 0) return gt;
+  return 1;
+}
+
+// Largest vector width (bytes) dividing every given byte count and address.
+int vec_width(std::initializer_list<long long> sizes, std::initializer_list<const void*> ptrs) {
+  for (int w = 16; w > 2; w >>= 1) {
+    bool ok = true;
+    for (long long s : sizes) ok = ok && (s % w == 0);
+    for (const void* p : ptrs) ok = ok && ((uintptr_t)p % w == 0);
+    if (ok) return w;
+  }
+  return 2;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tv_abi_version(void) { return 1; }
+
+const char* tv_last_error(void) { return g_err.c_str(); }
+
+size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_blocks,
+                                       int block_size, int partition_size) {
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0 ||
+      partition_size <= 0)
+    return 0;
+  const long long width = (long long)max_blocks * block_size;
+  const long long parts = (width + partition_size - 1) / partition_size;
+  if (parts <= 1) return 0;
+  return (size_t)num_seqs * num_heads * parts * (head_dim + 2) * sizeof(float);
+}
+
+int tv_paged_decode(void* out, const void* queries, const void* k_cache, const void* v_cache,
+                    const int32_t* block_tables, const int32_t* context_lens, int num_seqs, int num_heads,
+                    int num_kv_heads, int head_dim, int block_size, int num_blocks, int block_table_stride,
+                    int max_blocks, float scale, int dtype, int out_dtype, int partition_size, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (!out || !queries || !k_cache || !v_cache || !block_tables || !context_lens)
+    return fail(TV_EINVAL, "tv_paged_decode: null pointer argument");
+  if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
+    return fail(TV_EINVAL, "tv_paged_decode: bad dtype %d / out_dtype %d", dtype, out_dtype);
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(TV_EINVAL, "tv_paged_decode: bad head counts (num_seqs=%d, num_heads=%d, num_kv_heads=%d)",
+                num_seqs, num_heads, num_kv_heads);
+  if (block_size <= 0 || num_blocks <= 0 || block_table_stride <= 0 || max_blocks <= 0 ||
+      max_blocks > block_table_stride)
+    return fail(TV_EINVAL, "tv_paged_decode: bad block geometry (block_size=%d, num_blocks=%d, stride=%d, max_blocks=%d)",
+                block_size, num_blocks, block_table_stride, max_blocks);
+  if ((long long)max_blocks * block_size > (1LL << 30))
+    return fail(TV_EINVAL, "tv_paged_decode: context width too large");
+  if (partition_size <= 0 || partition_size % 16 != 0)
+    return fail(TV_EINVAL, "tv_paged_decode: partition_size must be a positive multiple of 16 (got %d)",
+                partition_size);
+  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(TV_EUNSUPPORTED, "tv_paged_decode: head_dim %d not supported (16/32/64/128/256)", head_dim);
+  if (dtype != TV_F32 && head_dim < 16)
+    return fail(TV_EUNSUPPORTED, "tv_paged_decode: head_dim %d too small", head_dim);
+
+  if ((uintptr_t)out % 16 || (uintptr_t)queries % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
+      (uintptr_t)block_tables % 4 || (uintptr_t)context_lens % 4)
+    return fail(TV_EINVAL, "tv_paged_decode: queries/caches/out must be 16-byte aligned");
+
+  const int group = num_heads / num_kv_heads;
+  const int gt = heads_per_group_chunk(group);
+  const long long width = (long long)max_blocks * block_size;
+  const int max_parts = (int)((width + partition_size - 1) / partition_size);
+  const size_t need = tv_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, max_blocks, block_size,
+                                                      partition_size);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(TV_EINVAL, "tv_paged_decode: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+
+  tv::DecodeParams p{};
+  p.out = out;
+  p.q = queries;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.block_tables = block_tables;
+  p.context_lens = context_lens;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.head_chunks = group / gt;
+  p.block_size = block_size;
+  p.bs_log2 = pow2(block_size) ? ilog2(block_size) : -1;
+  p.num_blocks = num_blocks;
+  p.bt_stride = block_table_stride;
+  p.max_blocks = max_blocks;
+  p.scale = scale;
+  p.partition_size = partition_size;
+  p.max_parts = max_parts;
+  p.out_dtype = out_dtype;
+  if (need > 0) {
+    const size_t n_o = (size_t)num_seqs * num_heads * max_parts * head_dim;
+    p.part_o = reinterpret_cast<float*>(workspace);
+    p.part_ml = p.part_o + n_o;
+  }
+  if (max_parts > 65535 || num_seqs > 65535 || num_kv_heads * p.head_chunks > 65535)
+    return fail(TV_EINVAL, "tv_paged_decode: grid too large");
+
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(max_parts, num_kv_heads * p.head_chunks, num_seqs);
+  bool launched = false;
+  if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, grid, s);
+  else if (dtype == TV_F16) launched = tv::launch_paged_decode<_Float16>(p, head_dim, gt, grid, s);
+  else launched = tv::launch_paged_decode<__bf16>(p, head_dim, gt, grid, s);
+  if (!launched) return fail(TV_EUNSUPPORTED, "tv_paged_decode: no kernel for head_dim=%d gt=%d", head_dim, gt);
+  int rc = check_launch("tv_paged_decode");
+  if (rc != TV_OK || max_parts <= 1) return rc;
+  hipLaunchKernelGGL(tv::paged_decode_reduce_kernel, dim3(num_heads, num_seqs), dim3(64), 0, s, p, head_dim);
+  return check_launch("tv_paged_decode(reduce)");
+}
+
+int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int q_len, int kv_len, int num_heads,
+                     int num_kv_heads, int head_dim, int head_dim_v, int64_t q_stride, int64_t k_stride,
+                     int64_t v_stride, int64_t out_stride, int causal, float scale, int dtype, int out_dtype,
+                     void* stream) {
+  if (!out || !q || !k || !v) return fail(TV_EINVAL, "tv_flash_prefill: null pointer argument");
+  if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
+    return fail(TV_EINVAL, "tv_flash_prefill: bad dtype %d / out_dtype %d", dtype, out_dtype);
+  if (q_len <= 0 || kv_len <= 0)
+    return fail(TV_EINVAL, "tv_flash_prefill: empty sequence (q_len=%d, kv_len=%d)", q_len, kv_len);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(TV_EINVAL, "tv_flash_prefill: bad head counts (%d, %d)", num_heads, num_kv_heads);
+  if (head_dim <= 0 || head_dim_v <= 0)
+    return fail(TV_EINVAL, "tv_flash_prefill: bad head dims (%d, %d)", head_dim, head_dim_v);
+  if (q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim ||
+      v_stride < (int64_t)num_kv_heads * head_dim_v || out_stride < (int64_t)num_heads * head_dim_v)
+    return fail(TV_EINVAL, "tv_flash_prefill: token stride smaller than a token row");
+  if (q_len > 65535 * 64 || num_heads > 65535)
+    return fail(TV_EINVAL, "tv_flash_prefill: grid too large");
+  tv::PrefillParams p{};
+  p.out = out;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.q_len = q_len;
+  p.kv_len = kv_len;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.head_dim = head_dim;
+  p.head_dim_v = head_dim_v;
+  p.q_stride = q_stride;
+  p.k_stride = k_stride;
+  p.v_stride = v_stride;
+  p.out_stride = out_stride;
+  p.causal = causal ? 1 : 0;
+  p.scale = scale;
+  p.out_dtype = out_dtype;
+  if (tv::launch_flash_prefill(p, dtype, true, reinterpret_cast<hipStream_t>(stream)) != 0)
+    return fail(TV_EUNSUPPORTED, "tv_flash_prefill: head_dim %d / %d not supported (max 256)", head_dim, head_dim_v);
+  return check_launch("tv_flash_prefill");
+}
+
+static int kv_write_common(const char* name, void* k_cache, void* v_cache, const void* k, const void* v,
+                           const int32_t* slots, int base_slot, int num_tokens, int num_kv_heads, int head_dim,
+                           int block_size, int num_blocks, int64_t k_stride, int64_t v_stride, int dtype,
+                           uint32_t* err_count, void* stream) {
+  if (!k_cache || !v_cache || !k || !v) return fail(TV_EINVAL, "%s: null pointer argument", name);
+  if (!valid_dtype(dtype)) return fail(TV_EINVAL, "%s: bad dtype %d", name, dtype);
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0)
+    return fail(TV_EINVAL, "%s: bad shape", name);
+  const long long row = (long long)num_kv_heads * head_dim;
+  if (k_stride < row || v_stride < row) return fail(TV_EINVAL, "%s: token stride smaller than a row", name);
+  if (num_tokens == 0) return ok();
+  const int es = elem_size(dtype);
+  const int w = vec_width({row * es, k_stride * es, v_stride * es}, {k_cache, v_cache, k, v});
+  tv::KVWriteParams p{};
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.k = k;
+  p.v = v;
+  p.slots = slots;
+  p.base_slot = base_slot;
+  p.num_tokens = num_tokens;
+  p.row_vecs = (int)(row * es / w);
+  p.k_stride = k_stride * es / w;
+  p.v_stride = v_stride * es / w;
+  p.num_slots = (long long)num_blocks * block_size;
+  p.err_count = err_count;
+  tv::launch_kv_write(p, w, reinterpret_cast<hipStream_t>(stream));
+  return check_launch(name);
+}
+
+int tv_reshape_and_cache(void* k_cache, void* v_cache, const void* k, const void* v, const int32_t* slot_mapping,
+                         int num_tokens, int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                         int64_t k_stride, int64_t v_stride, int dtype, uint32_t* err_count, void* stream) {
+  if (!slot_mapping && num_tokens > 0) return fail(TV_EINVAL, "tv_reshape_and_cache: null slot_mapping");
+  return kv_write_common("tv_reshape_and_cache", k_cache, v_cache, k, v, slot_mapping, 0, num_tokens, num_kv_heads,
+                         head_dim, block_size, num_blocks, k_stride, v_stride, dtype, err_count, stream);
+}
+
+int tv_write_kv(void* k_cache, void* v_cache, const void* k, const void* v, int block_id, int start_offset,
+                int num_tokens, int num_kv_heads, int head_dim, int block_size, int num_blocks, int64_t k_stride,
+                int64_t v_stride, int dtype, void* stream) {
+  if (block_id < 0 || block_id >= num_blocks)
+    return fail(TV_EINVAL, "tv_write_kv: block_id %d outside [0, %d)", block_id, num_blocks);
+  if (start_offset < 0 || num_tokens < 0 || start_offset + num_tokens > block_size)
+    return fail(TV_EINVAL, "tv_write_kv: rows [%d, %d) do not fit a block of %d", start_offset,
+                start_offset + num_tokens, block_size);
+  return kv_write_common("tv_write_kv", k_cache, v_cache, k, v, nullptr, block_id * block_size + start_offset,
+                         num_tokens, num_kv_heads, head_dim, block_size, num_blocks, k_stride, v_stride, dtype,
+                         nullptr, stream);
+}
+
+int tv_read_kv_blocks(void* k_out, void* v_out, const void* k_cache, const void* v_cache, const int32_t* block_ids,
+                      int num_block_ids, int context_len, int num_kv_heads, int head_dim, int block_size,
+                      int num_blocks, int dtype, void* stream) {
+  if (!valid_dtype(dtype)) return fail(TV_EINVAL, "tv_read_kv_blocks: bad dtype %d", dtype);
+  if (context_len < 0 || num_block_ids < 0 || (long long)context_len > (long long)num_block_ids * block_size)
+    return fail(TV_EINVAL, "tv_read_kv_blocks: context_len %d exceeds %d blocks of %d", context_len, num_block_ids,
+                block_size);
+  if (context_len == 0) return ok();
+  if (!k_out || !v_out || !k_cache || !v_cache || !block_ids)
+    return fail(TV_EINVAL, "tv_read_kv_blocks: null pointer argument");
+  const int es = elem_size(dtype);
+  const long long row = (long long)num_kv_heads * head_dim * es;
+  const int w = vec_width({row}, {k_out, v_out, k_cache, v_cache});
+  tv::KVGatherParams p{};
+  p.k_out = k_out;
+  p.v_out = v_out;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.block_ids = block_ids;
+  p.context_len = context_len;
+  p.block_size = block_size;
+  p.row_vecs = (int)(row / w);
+  p.num_blocks = num_blocks;
+  tv::launch_kv_gather(p, w, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("tv_read_kv_blocks");
+}
+
+}  // extern "C"

@@ -1,0 +1,136 @@
+// Shared device helpers for the tinyvllm MI355X (gfx950) attention kernels.
+//
+// Element types: float, _Float16, __bf16.  All global loads and stores of
+// cache / activation rows go through 16-byte vectors (u32x4) so every lane
+// issues one 128-bit access.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tv {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+template <typename T> struct ElemTraits;
+template <> struct ElemTraits<float> { static constexpr int kCode = kF32; };
+template <> struct ElemTraits<_Float16> { static constexpr int kCode = kF16; };
+template <> struct ElemTraits<__bf16> { static constexpr int kCode = kBF16; };
+
+// ---- conversions on packed 32-bit words -----------------------------------
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(f16x2, w)[0];
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(f16x2, w)[1];
+}
+
+// Unpack the two elements of a 32-bit word of type T into floats.
+template <typename T> __device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b);
+template <> __device__ __forceinline__ void unpack2<_Float16>(uint32_t w, float& a, float& b) {
+  a = f16_lo(w); b = f16_hi(w);
+}
+template <> __device__ __forceinline__ void unpack2<__bf16>(uint32_t w, float& a, float& b) {
+  a = bf16_lo(w); b = bf16_hi(w);
+}
+
+// Dot product of two packed pairs accumulated in fp32 (v_dot2_f32_{f16,bf16}).
+template <typename T> __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c);
+template <> __device__ __forceinline__ float dot2<_Float16>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
+template <> __device__ __forceinline__ float dot2<__bf16>(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// Round a float to T (round-to-nearest-even) and back to raw bits.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <typename T> __device__ __forceinline__ T from_float(float f);
+template <> __device__ __forceinline__ float from_float<float>(float f) { return f; }
+template <> __device__ __forceinline__ _Float16 from_float<_Float16>(float f) { return (_Float16)f; }
+template <> __device__ __forceinline__ __bf16 from_float<__bf16>(float f) {
+  return __builtin_bit_cast(__bf16, f32_to_bf16_bits(f));
+}
+
+template <typename T> __device__ __forceinline__ float to_float(T x);
+template <> __device__ __forceinline__ float to_float<float>(float x) { return x; }
+template <> __device__ __forceinline__ float to_float<_Float16>(_Float16 x) { return (float)x; }
+template <> __device__ __forceinline__ float to_float<__bf16>(__bf16 x) {
+  return __builtin_bit_cast(float, (uint32_t)__builtin_bit_cast(uint16_t, x) << 16);
+}
+
+// Store one float as the output dtype selected at run time.
+__device__ __forceinline__ void store_as(void* base, size_t idx, float v, int dtype) {
+  if (dtype == kF32) {
+    reinterpret_cast<float*>(base)[idx] = v;
+  } else if (dtype == kF16) {
+    reinterpret_cast<_Float16*>(base)[idx] = (_Float16)v;
+  } else {
+    reinterpret_cast<uint16_t*>(base)[idx] = f32_to_bf16_bits(v);
+  }
+}
+
+// ---- wave64 cross-lane helpers ---------------------------------------------
+// DPP controls (GFX9 encoding): quad_perm, row_half_mirror, row_mirror.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within each 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within each 16
+
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float shfl_xor(float x, int mask) {
+  int lane = __lane_id();
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
+}
+
+// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of the
+// group receives the total.  Groups of up to 16 use DPP only.
+template <int N> __device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp<kDppXor1>(x);
+  if constexpr (N >= 4) x += dpp<kDppXor2>(x);
+  if constexpr (N >= 8) x += dpp<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp<kDppMirror>(x);
+  if constexpr (N >= 32) x += shfl_xor(x, 16);
+  if constexpr (N >= 64) x += shfl_xor(x, 32);
+  return x;
+}
+
+template <int N> __device__ __forceinline__ float group_max(float x) {
+  if constexpr (N >= 2) x = fmaxf(x, dpp<kDppXor1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp<kDppXor2>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp<kDppMirror>(x));
+  if constexpr (N >= 32) x = fmaxf(x, shfl_xor(x, 16));
+  if constexpr (N >= 64) x = fmaxf(x, shfl_xor(x, 32));
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace tv
