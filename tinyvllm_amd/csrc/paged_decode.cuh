@@ -159,7 +159,7 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             if constexpr (sizeof(T) == 4) {
-              d = fmaf(__builtin_bit_cast(float, qv[g][v][w]), __builtin_bit_cast(float, kr[j][v][w]), d);
+              d = fmaf(u32_as_f32(qv[g][v][w]), u32_as_f32(kr[j][v][w]), d);
             } else {
               d = dot2<T>(qv[g][v][w], kr[j][v][w], d);
             }
@@ -200,7 +200,7 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           if constexpr (sizeof(T) == 4) {
-            vf[v * EPV + w] = __builtin_bit_cast(float, vr[j][v][w]);
+            vf[v * EPV + w] = u32_as_f32(vr[j][v][w]);
           } else {
             unpack2<T>(vr[j][v][w], vf[v * EPV + 2 * w], vf[v * EPV + 2 * w + 1]);
           }

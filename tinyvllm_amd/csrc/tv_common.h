@@ -30,6 +30,11 @@ template <> struct ElemTraits<__bf16> { static constexpr int kCode = kBF16; };
 
 // ---- conversions on packed 32-bit words -----------------------------------
 
+// Reinterpret a 32-bit word as float.  Takes the word by value: applying
+// __builtin_bit_cast directly to an element of an ext_vector_type lvalue reads
+// element 0 of the vector with this compiler.
+__device__ __forceinline__ float u32_as_f32(uint32_t w) { return __builtin_bit_cast(float, w); }
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 __device__ __forceinline__ float f16_lo(uint32_t w) {
