@@ -149,7 +149,7 @@ def test_invalid_block_id_gives_nan_not_fault():
     bt[1, 1] = kc.shape[0] + 1000                 # outside the cache
     out = run(q, kc, vc, bt, cl, 8, 2, 64, 16).cpu().numpy()
     assert np.isnan(out[1]).all()
-    want = oracle(q, kc, vc, bt[:1], cl[:1], 8, 2, 64, 16)
+    want = oracle(q[:1], kc, vc, bt[:1], cl[:1], 8, 2, 64, 16)
     assert np.abs(out[:1] - want).max() <= 1e-4
 
 
