@@ -14,7 +14,11 @@
 //   partial sums are combined across the LPR lanes of a row with DPP; lanes of
 //   one row form a "group" that runs its own online softmax (running max m,
 //   running sum l, unnormalised accumulator acc) in the log2 domain.
-//   Groups and waves are merged once at the end (shuffles, then LDS).
+//   Groups and waves are merged once at the end (DPP / swizzle, then LDS).
+//   Split-context partials (m, l, o) go to the caller's workspace and a second
+//   kernel merges them (flash-decoding).
+//   When a cache block holds whole tiles (block_size % 16 == 0) each tile needs
+//   a single wave-uniform block-table lookup.
 //
 // Semantics follow tinyvllm/model/llama.py:97-144: scores are (q.k)*scale,
 // positions >= context_len are excluded (the reference adds -1e9, which
@@ -26,6 +30,26 @@
 #pragma once
 
 #include "tv_common.h"
+
+// Build-time tuning knobs (defaults are the tuned values for gfx950).
+#ifndef TV_DECODE_TILE_MUL
+#define TV_DECODE_TILE_MUL 1     // rows per lane per tile multiplier (tile = 16 * this tokens)
+#endif
+#ifndef TV_DECODE_NT
+#define TV_DECODE_NT 1           // non-temporal K/V loads
+#endif
+#ifndef TV_DECODE_ACC_MAX
+#define TV_DECODE_ACC_MAX 64     // max fp32 accumulators per lane (sets lanes per row)
+#endif
+#ifndef TV_DECODE_MIN_BLOCKS
+#define TV_DECODE_MIN_BLOCKS 1   // occupancy hint: work-groups per CU the VGPR budget must allow
+#endif
+#ifndef TV_DECODE_BT_PREFETCH
+#define TV_DECODE_BT_PREFETCH 0  // look the next tile's block id up one tile ahead
+#endif
+#ifndef TV_DECODE_PREFETCH
+#define TV_DECODE_PREFETCH 0     // register double-buffering of the next tile
+#endif
 
 namespace tv {
 
@@ -59,24 +83,85 @@ __device__ __forceinline__ int decode_len(const DecodeParams& p, int b, float& b
   return ctx <= 0 ? width : (ctx < width ? ctx : width);
 }
 
-template <typename T, int D, int GT, int NW>
-__global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParams p) {
-  constexpr int ROW_BYTES = D * (int)sizeof(T);
-  constexpr int LPR = ROW_BYTES / 16 < 16 ? ROW_BYTES / 16 : 16;
-  constexpr int VPL = ROW_BYTES / (16 * LPR);
-  constexpr int RPI = 64 / LPR;
-  constexpr int NR = RPI >= 16 ? 1 : 16 / RPI;
-  constexpr int TT = RPI * NR;
-  constexpr int EPV = 16 / (int)sizeof(T);
-  constexpr int EPL = VPL * EPV;
+// Compile-time lane layout of the decode kernel for element type T, head_dim D
+// and GT query heads per work-group.
+//   LPR  lanes per cache row; chosen so each lane keeps at most 64 fp32
+//        accumulators (GT * D / LPR <= 64), capped at 16 (one DPP row) and at
+//        one 16-byte vector per lane.
+//   VPL  16-byte vectors per lane per row (lane c holds vectors c, c+LPR, ...,
+//        so every load instruction covers LPR*16 contiguous bytes of a row).
+//   RPI  rows fetched by one load instruction; NR rows per lane per tile;
+//        TT = RPI*NR tokens per wave-tile (16 unless a row needs < 4 lanes).
+template <typename T, int D, int GT>
+struct DecodeShape {
+  static constexpr int ROW_BYTES = D * (int)sizeof(T);
+  static constexpr int MAXL = ROW_BYTES / 16 < 16 ? ROW_BYTES / 16 : 16;
+  static constexpr int WANT = D * GT / TV_DECODE_ACC_MAX < 1 ? 1 : D * GT / TV_DECODE_ACC_MAX;
+  static constexpr int LPR = WANT < MAXL ? WANT : MAXL;
+  static constexpr int VPL = ROW_BYTES / (16 * LPR);
+  static constexpr int RPI = 64 / LPR;
+  static constexpr int NR = (RPI >= 16 ? 1 : 16 / RPI) * TV_DECODE_TILE_MUL;
+  static constexpr int TT = RPI * NR;
+  static constexpr int EPV = 16 / (int)sizeof(T);
+  static constexpr int EPL = VPL * EPV;
   static_assert(LPR >= 1 && VPL >= 1 && LPR * VPL * 16 == ROW_BYTES, "unsupported row size");
+};
 
-  __shared__ float sh_acc[NW][GT][D];
+// 16-byte cache-row load; K/V rows are read exactly once per launch, so they
+// can bypass cache retention (TV_DECODE_NT).
+__device__ __forceinline__ u32x4 load_row16(const void* ptr) {
+#if TV_DECODE_NT
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
+#else
+  return *reinterpret_cast<const u32x4*>(ptr);
+#endif
+}
+
+// Running maxima are only raised when a tile's maximum exceeds them by more
+// than this many log2 units, so most tiles skip the rescale of l and acc; the
+// unnormalised weights stay <= 2^kRescaleSlack, far from fp32 overflow.
+constexpr float kRescaleSlack = 8.0f;
+
+template <int CTRL, int N> __device__ __forceinline__ void dpp_add_arr(float (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp<CTRL>(x[i]);
+}
+
+// All-reduce sum over aligned groups of G lanes (G <= 16) for N independent
+// values; the steps are interleaved across the values so no DPP hazard stalls.
+template <int G, int N> __device__ __forceinline__ void group_sum_arr(float (&x)[N]) {
+  if constexpr (G >= 2) dpp_add_arr<kDppXor1>(x);
+  if constexpr (G >= 4) dpp_add_arr<kDppXor2>(x);
+  if constexpr (G >= 8) dpp_add_arr<kDppHalfMirror>(x);
+  if constexpr (G >= 16) dpp_add_arr<kDppMirror>(x);
+}
+
+// Sum over the lanes of each 16-lane row that share lane % G (G <= 16 a power
+// of two), using row rotations; every lane receives its class total.
+template <int G> __device__ __forceinline__ float row_class_sum(float x) {
+  if constexpr (G <= 1) x += dpp<0x121>(x);   // row_ror:1
+  if constexpr (G <= 2) x += dpp<0x122>(x);   // row_ror:2
+  if constexpr (G <= 4) x += dpp<0x124>(x);   // row_ror:4
+  if constexpr (G <= 8) x += dpp<0x128>(x);   // row_ror:8
+  return x;
+}
+
+__device__ __forceinline__ float swizzle_xor16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+}
+
+template <typename T, int D, int GT, int NW>
+__global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_kernel(const DecodeParams p) {
+  using S = DecodeShape<T, D, GT>;
+  constexpr int LPR = S::LPR, VPL = S::VPL, RPI = S::RPI, NR = S::NR, TT = S::TT;
+  constexpr int EPV = S::EPV, EPL = S::EPL;
+
+  __shared__ float sh_acc[NW][2][GT][D];   // per wave, per 32-lane half
+  __shared__ float sh_l[NW][2][GT];
   __shared__ float sh_m[NW][GT];
-  __shared__ float sh_l[NW][GT];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r = lane / LPR;
   const int c = lane % LPR;
@@ -94,9 +179,11 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
   const int end = min(start + p.partition_size, len);
 
   const T* qp = reinterpret_cast<const T*>(p.q) + ((size_t)b * p.num_heads + h0) * D;
-  const T* kc = reinterpret_cast<const T*>(p.k_cache);
-  const T* vc = reinterpret_cast<const T*>(p.v_cache);
+  const T* kc = reinterpret_cast<const T*>(p.k_cache) + (size_t)kh * D;
+  const T* vc = reinterpret_cast<const T*>(p.v_cache) + (size_t)kh * D;
   const int* bt = p.block_tables + (size_t)b * p.bt_stride;
+  const size_t row_stride = (size_t)p.num_kv_heads * D;          // elements between cache rows
+  const bool uniform_block = p.block_size % TT == 0 && p.partition_size % TT == 0 && p.bs_log2 >= 0;
 
   u32x4 qv[GT][VPL];
 #pragma unroll
@@ -114,41 +201,84 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
   }
   bool bad = false;
-  const float scale = p.scale;
+  const float sc = p.scale * kLog2e;
+  const float bi2 = bias * kLog2e;
 
-  for (int t0 = start + wave * TT; t0 < end; t0 += NW * TT) {
-    u32x4 kr[NR][VPL], vr[NR][VPL];
-    bool valid[NR];
+  // Fetch the K/V rows of the tile starting at token t0 (rows past `end` or in
+  // an invalid block are zero and marked invalid).
+  constexpr bool kBtAhead = TV_DECODE_BT_PREFETCH && !TV_DECODE_PREFETCH;
+  auto fetch = [&](int t0, int blk_ahead, u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR]) {
+    if (uniform_block) {
+      // the whole tile lies in one cache block: one wave-uniform table lookup
+      const int blk = kBtAhead ? blk_ahead : bt[t0 >> p.bs_log2];
+      const bool blk_ok = (unsigned)blk < (unsigned)p.num_blocks;
+      bad |= !blk_ok;
+      const size_t base = ((size_t)blk * p.block_size + (t0 & (p.block_size - 1)) + r) * row_stride;
+      if (blk_ok && t0 + TT <= end) {
+        // full tile: no per-row predication
 #pragma unroll
-    for (int j = 0; j < NR; ++j) {
-      const int pos = t0 + j * RPI + r;
-      valid[j] = pos < end;
-      size_t base = 0;
-      if (valid[j]) {
-        const int bi = p.bs_log2 >= 0 ? (pos >> p.bs_log2) : pos / p.block_size;
-        const int off = pos - bi * p.block_size;
-        const int blk = bt[bi];
-        if ((unsigned)blk >= (unsigned)p.num_blocks) {
-          bad = true;
-          valid[j] = false;
-        } else {
-          base = (((size_t)blk * p.block_size + off) * p.num_kv_heads + kh) * D;
+        for (int j = 0; j < NR; ++j) {
+          valid[j] = true;
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) {
+            const size_t off = base + (size_t)j * RPI * row_stride + (v * LPR + c) * EPV;
+            kr[j][v] = load_row16(kc + off);
+            vr[j][v] = load_row16(vc + off);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+          valid[j] = blk_ok && (t0 + j * RPI + r < end);
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) {
+            const size_t off = base + (size_t)j * RPI * row_stride + (v * LPR + c) * EPV;
+            if (valid[j]) {
+              kr[j][v] = load_row16(kc + off);
+              vr[j][v] = load_row16(vc + off);
+            } else {
+              kr[j][v] = u32x4{0, 0, 0, 0};
+              vr[j][v] = u32x4{0, 0, 0, 0};
+            }
+          }
         }
       }
+    } else {
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
+      for (int j = 0; j < NR; ++j) {
+        const int pos = t0 + j * RPI + r;
+        valid[j] = pos < end;
+        size_t base = 0;
         if (valid[j]) {
-          kr[j][v] = *reinterpret_cast<const u32x4*>(kc + base + (v * LPR + c) * EPV);
-          vr[j][v] = *reinterpret_cast<const u32x4*>(vc + base + (v * LPR + c) * EPV);
-        } else {
-          kr[j][v] = u32x4{0, 0, 0, 0};
-          vr[j][v] = u32x4{0, 0, 0, 0};
+          const int bi = p.bs_log2 >= 0 ? (pos >> p.bs_log2) : pos / p.block_size;
+          const int off = pos - bi * p.block_size;
+          const int blk = bt[bi];
+          if ((unsigned)blk >= (unsigned)p.num_blocks) {
+            bad = true;
+            valid[j] = false;
+          } else {
+            base = ((size_t)blk * p.block_size + off) * row_stride;
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          if (valid[j]) {
+            kr[j][v] = load_row16(kc + base + (v * LPR + c) * EPV);
+            vr[j][v] = load_row16(vc + base + (v * LPR + c) * EPV);
+          } else {
+            kr[j][v] = u32x4{0, 0, 0, 0};
+            vr[j][v] = u32x4{0, 0, 0, 0};
+          }
         }
       }
     }
 
-    // scores (log2 domain) for NR rows x GT heads
-    float s[NR][GT];
+  };
+
+  // Scores, online-softmax update and P.V accumulation for one fetched tile.
+  auto consume = [&](u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR]) {
+    // partial q.k over this lane's slice, then all-reduce over the LPR lanes of the row
+    float s[NR * GT];
 #pragma unroll
     for (int j = 0; j < NR; ++j) {
 #pragma unroll
@@ -165,30 +295,49 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
             }
           }
         }
-        d = group_sum<LPR>(d);
-        s[j][g] = valid[j] ? fmaf(d, scale, bias) * kLog2e : kNegInf;
+        s[j * GT + g] = d;
       }
     }
+    group_sum_arr<LPR>(s);
+#pragma unroll
+    for (int j = 0; j < NR; ++j)
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+        s[j * GT + g] = valid[j] ? fmaf(s[j * GT + g], sc, bi2) : kNegInf;
 
-    // online softmax update per head
+    // raise the running maxima only when a tile exceeds them by the slack
+    float mt[GT];
+    bool raise = false;
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
-      float mt = s[0][g];
+      mt[g] = s[g];
 #pragma unroll
-      for (int j = 1; j < NR; ++j) mt = fmaxf(mt, s[j][g]);
-      const float mn = fmaxf(m[g], mt);
-      const float mu = mn == kNegInf ? 0.0f : mn;
-      const float alpha = fast_exp2(m[g] - mu);
-      m[g] = mn;
-      float ls = l[g] * alpha;
+      for (int j = 1; j < NR; ++j) mt[g] = fmaxf(mt[g], s[j * GT + g]);
+      raise |= mt[g] > m[g] + kRescaleSlack;
+    }
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      // opaque to the optimiser: keeps this rarely taken block a real branch
+      // instead of an if-converted multiply of every accumulator per tile
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        const float mn = mt[g] > m[g] + kRescaleSlack ? fmaxf(m[g], mt[g]) : m[g];
+        const float alpha = mn == kNegInf ? 1.0f : fast_exp2(m[g] - mn);
+        m[g] = mn;
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float mu = m[g] == kNegInf ? 0.0f : m[g];
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
-        s[j][g] = fast_exp2(s[j][g] - mu);
-        ls += s[j][g];
+        const float pj = fast_exp2(s[j * GT + g] - mu);
+        s[j * GT + g] = pj;
+        l[g] += pj;
       }
-      l[g] = ls;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
     }
 
     // acc += p * v
@@ -209,41 +358,77 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
 #pragma unroll
       for (int g = 0; g < GT; ++g)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(s[j][g], vf[e], acc[g][e]);
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(s[j * GT + g], vf[e], acc[g][e]);
+    }
+  };
+
+#if TV_DECODE_PREFETCH
+  {
+    u32x4 ka[NR][VPL], va[NR][VPL], kb[NR][VPL], vb[NR][VPL];
+    bool oka[NR], okb[NR];
+    int t0 = start + wave * TT;
+    if (t0 < end) fetch(t0, 0, ka, va, oka);
+    while (t0 < end) {
+      const int t1 = t0 + NW * TT;
+      if (t1 < end) fetch(t1, 0, kb, vb, okb);
+      consume(ka, va, oka);
+      if (t1 >= end) break;
+      const int t2 = t1 + NW * TT;
+      if (t2 < end) fetch(t2, 0, ka, va, oka);
+      consume(kb, vb, okb);
+      t0 = t2;
     }
   }
+#else
+  int blk_next = 0;
+  if (kBtAhead && uniform_block && start + wave * TT < end) blk_next = bt[(start + wave * TT) >> p.bs_log2];
+  for (int t0 = start + wave * TT; t0 < end; t0 += NW * TT) {
+    u32x4 kr[NR][VPL], vr[NR][VPL];
+    bool valid[NR];
+    const int blk_cur = blk_next;
+    if (kBtAhead && uniform_block && t0 + NW * TT < end) blk_next = bt[(t0 + NW * TT) >> p.bs_log2];
+    fetch(t0, blk_cur, kr, vr, valid);
+    consume(kr, vr, valid);
+  }
+#endif
 
-  // merge the RPI row groups of this wave (lanes with equal c)
+  // ---- merge row groups and waves ------------------------------------------
+  // 1) common maximum per head across the wave; rescale each group onto it
 #pragma unroll
-  for (int msk = LPR; msk < 64; msk <<= 1) {
+  for (int g = 0; g < GT; ++g) {
+    float mw = m[g];
 #pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      const float mo = shfl_xor(m[g], msk);
-      const float lo = shfl_xor(l[g], msk);
-      const float mn = fmaxf(m[g], mo);
-      const float mu = mn == kNegInf ? 0.0f : mn;
-      const float fa = fast_exp2(m[g] - mu);
-      const float fb = fast_exp2(mo - mu);
-      l[g] = l[g] * fa + lo * fb;
+    for (int msk = LPR; msk < 64; msk <<= 1) mw = fmaxf(mw, shfl_xor(mw, msk));
+    const float f = mw == kNegInf ? 0.0f : fast_exp2(m[g] - mw);
+    l[g] *= f;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float ao = shfl_xor(acc[g][e], msk);
-        acc[g][e] = acc[g][e] * fa + ao * fb;
-      }
-      m[g] = mn;
+    for (int e = 0; e < EPL; ++e) acc[g][e] *= f;
+    m[g] = mw;
+  }
+  // 2) sum the groups of each 16-lane row (lanes with equal c), then the two
+  //    rows of each 32-lane half
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    if constexpr (LPR < 16) l[g] = row_class_sum<LPR>(l[g]);
+    l[g] += swizzle_xor16(l[g]);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      if constexpr (LPR < 16) acc[g][e] = row_class_sum<LPR>(acc[g][e]);
+      acc[g][e] += swizzle_xor16(acc[g][e]);
     }
   }
-
-  if (lane < LPR) {
+  // 3) lanes 0..LPR-1 and 32..32+LPR-1 publish their half's partial sums
+  const int half = lane >> 5;
+  if ((lane & 31) < LPR) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) sh_acc[wave][g][(v * LPR + c) * EPV + e] = acc[g][v * EPV + e];
+        for (int e = 0; e < EPV; ++e) sh_acc[wave][half][g][(v * LPR + c) * EPV + e] = acc[g][v * EPV + e];
       if (c == 0) {
-        sh_m[wave][g] = m[g];
-        sh_l[wave][g] = l[g];
+        sh_l[wave][half][g] = l[g];
+        if (half == 0) sh_m[wave][g] = m[g];
       }
     }
   }
@@ -261,8 +446,8 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float f = fast_exp2(sh_m[w][g] - Mu);
-      L += sh_l[w][g] * f;
-      O += sh_acc[w][g][d] * f;
+      L += (sh_l[w][0][g] + sh_l[w][1][g]) * f;
+      O += (sh_acc[w][0][g][d] + sh_acc[w][1][g][d]) * f;
     }
     const int h = h0 + g;
     if (nparts == 1) {
@@ -283,5 +468,6 @@ __global__ void __launch_bounds__(64 * NW) paged_decode_kernel(const DecodeParam
 // grid (Hq, B) and 64 threads; sequences that fit one partition were written by
 // the main kernel and are skipped here.
 __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodeParams p, int head_dim);
+
 
 }  // namespace tv

@@ -7,7 +7,10 @@
 
 namespace tv {
 
-constexpr int kDecodeWaves = 4;
+#ifndef TV_DECODE_WAVES
+#define TV_DECODE_WAVES 4
+#endif
+constexpr int kDecodeWaves = TV_DECODE_WAVES;   // waves per work-group
 
 // Launch the main kernel for element type T.  Returns false when (D, GT) has no
 // instantiation.

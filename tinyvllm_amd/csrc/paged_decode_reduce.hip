@@ -19,23 +19,50 @@ __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodePar
 
   const size_t base = ((size_t)b * p.num_heads + h) * p.max_parts;
   const float* ml = p.part_ml + base * 2;
+  const float* po = p.part_o + base * head_dim;
+  const int lane = threadIdx.x;
+  // global maximum over the partitions (lane i reads partitions i, i+64, ...)
   float M = kNegInf;
   bool nan_seen = false;
-  for (int i = 0; i < nparts; ++i) {
+  for (int i = lane; i < nparts; i += 64) {
     const float mi = ml[2 * i];
     nan_seen |= (mi != mi);
     M = fmaxf(M, mi);
   }
+  M = group_max<64>(M);
+  nan_seen = __builtin_amdgcn_ballot_w64(nan_seen) != 0;
   const float Mu = M == kNegInf ? 0.0f : M;
-  for (int d = threadIdx.x; d < head_dim; d += 64) {
-    float num = 0.0f, den = 0.0f;
-    for (int i = 0; i < nparts; ++i) {
-      const float w = ml[2 * i + 1] * fast_exp2(ml[2 * i] - Mu);
-      num = fmaf(w, p.part_o[(base + i) * head_dim + d], num);
+  // per-partition weights w_i = L_i * 2^(M_i - M) through LDS, in chunks of 256
+  __shared__ float sw[256];
+  float num[4] = {0.f, 0.f, 0.f, 0.f};
+  float den = 0.0f;
+  for (int c0 = 0; c0 < nparts; c0 += 256) {
+    const int cn = min(256, nparts - c0);
+    __syncthreads();
+    for (int i = lane; i < cn; i += 64) {
+      const float w = ml[2 * (c0 + i) + 1] * fast_exp2(ml[2 * (c0 + i)] - Mu);
+      sw[i] = w;
       den += w;
     }
-    const float val = nan_seen ? __builtin_nanf("") : num / den;
-    store_as(p.out, ((size_t)b * p.num_heads + h) * head_dim + d, val, p.out_dtype);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int d = lane + 64 * t;
+      if (d < head_dim) {
+        float a = num[t];
+#pragma unroll 4
+        for (int i = 0; i < cn; ++i) a = fmaf(sw[i], po[(size_t)(c0 + i) * head_dim + d], a);
+        num[t] = a;
+      }
+    }
+  }
+  den = group_sum<64>(den);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int d = lane + 64 * t;
+    if (d < head_dim)
+      store_as(p.out, ((size_t)b * p.num_heads + h) * head_dim + d, nan_seen ? __builtin_nanf("") : num[t] / den,
+               p.out_dtype);
   }
 }
 

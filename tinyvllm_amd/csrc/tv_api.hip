@@ -155,8 +155,9 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   if (!launched) return fail(TV_EUNSUPPORTED, "tv_paged_decode: no kernel for head_dim=%d gt=%d", head_dim, gt);
   int rc = check_launch("tv_paged_decode");
   if (rc != TV_OK || max_parts <= 1) return rc;
+  if (head_dim > 256) return fail(TV_EUNSUPPORTED, "tv_paged_decode: merge supports head_dim <= 256");
   hipLaunchKernelGGL(tv::paged_decode_reduce_kernel, dim3(num_heads, num_seqs), dim3(64), 0, s, p, head_dim);
-  return check_launch("tv_paged_decode(reduce)");
+  return check_launch("tv_paged_decode(merge)");
 }
 
 int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int q_len, int kv_len, int num_heads,
