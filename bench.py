@@ -36,6 +36,12 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
+# HBM bytes per launch of the primary decode kernel measured with two rocprofv3
+# --pmc passes (FETCH_SIZE x2.000 + WRITE_SIZE x1.000, factors from a plain
+# 1 GiB copy), recorded in profiles/paged_decode_llama3_8b_f16.md.
+PRIMARY_TRAFFIC_BYTES = 2501465088
+PRIMARY_TRAFFIC_SOURCE = "profiles/paged_decode_llama3_8b_f16.md"
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
@@ -157,6 +163,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--primary-only", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -193,6 +201,16 @@ def main():
         del wl5
         configs["e2e_tinyllama_decode"] = {"value": None, "unit": "tok/s", "note": "not built yet"}
 
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copy of {n} bytes done")
+        del src, dst
+
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: cpu baseline (oracle float32 restatement)")
@@ -216,7 +234,8 @@ def main():
                    "sum_ctx": int(wl3.context_lens.astype(np.int64).sum()),
                    "partition_size": r3["partition_size"]},
         "roofline": {"bound": "hbm", "achieved": round(r3["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r3["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(r3["gbs"] / HBM_PEAK_GBS, 4), "traffic": PRIMARY_TRAFFIC_BYTES,
+                     "traffic_source": PRIMARY_TRAFFIC_SOURCE,
                      "algorithmic_bytes_per_launch": r3["bytes"],
                      "timing": "HIP events over K launches of decode+merge on the launch stream"},
         "cpu_baseline": cpu,
