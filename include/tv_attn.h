@@ -85,14 +85,23 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
  * (tinyvllm/model/llama.py:58-94) with the batch dimension (always 1 there)
  * removed.  causal != 0 excludes key j for query i when j > i (top-left
  * aligned, llama.py:86-90).  head_dim_v may differ from head_dim (generic
- * kernel); fp16/bf16 with head_dim in {64,128} and head_dim_v == head_dim run
- * on MFMA.  Strides are in elements between consecutive tokens.
+ * kernel); fp16/bf16 with head_dim in {64,128}, head_dim_v == head_dim and
+ * 16-byte aligned rows run on MFMA.  Strides are in elements between
+ * consecutive tokens.
+ * chunk_tiles: key tiles (of 64) per work unit; long causal rows are split into
+ * chunks processed by separate work-groups and merged by a second kernel, which
+ * needs `workspace` of tv_flash_prefill_workspace_bytes(...) bytes (0 = no
+ * split).  chunk_tiles <= 0 picks a size from the shape.
  */
+size_t tv_flash_prefill_workspace_bytes(int q_len, int kv_len, int num_heads, int head_dim, int head_dim_v,
+                                        int causal, int dtype, int chunk_tiles);
+
 int tv_flash_prefill(void* out, const void* q, const void* k, const void* v,
                      int q_len, int kv_len, int num_heads, int num_kv_heads,
                      int head_dim, int head_dim_v,
                      int64_t q_stride, int64_t k_stride, int64_t v_stride, int64_t out_stride,
-                     int causal, float scale, int dtype, int out_dtype, void* stream);
+                     int causal, float scale, int dtype, int out_dtype,
+                     int chunk_tiles, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Fused K/V cache write from a slot mapping.  Replaces the per-chunk

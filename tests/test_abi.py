@@ -46,6 +46,10 @@ def test_argument_counts_match_header():
 
 def test_workspace_size_is_host_arithmetic():
     lib = _lib.load()
+    # prefill: L=1024 causal, 32 heads, D=64, chunks of 4 key tiles -> 16 q tiles x 4 chunks x 64 rows x 66 floats
+    assert lib.tv_flash_prefill_workspace_bytes(1024, 1024, 32, 64, 64, 1, 1, 4) == 32 * 16 * 4 * 64 * 66 * 4
+    assert lib.tv_flash_prefill_workspace_bytes(1024, 1024, 32, 64, 64, 1, 1, 0) == 0      # default: no split
+    assert lib.tv_flash_prefill_workspace_bytes(1024, 1024, 32, 64, 64, 1, 0, 4) == 0      # fp32: generic kernel
     assert lib.tv_paged_decode_workspace_bytes(4, 32, 64, 16, 16, 512) == 0      # one partition
     # 256 seqs x 32 heads x 8 partitions x (128 + 2) floats
     assert lib.tv_paged_decode_workspace_bytes(256, 32, 128, 256, 16, 512) == 256 * 32 * 8 * 130 * 4
@@ -74,7 +78,7 @@ def test_validation_errors_are_reported_without_launch():
     rc = lib.tv_write_kv(fake, fake, fake, fake, 0, 10, 7, 4, 64, 16, 10, 256, 256, 1, None)
     assert rc == _lib.TV_EINVAL and b"do not fit" in lib.tv_last_error()
     rc = lib.tv_flash_prefill(fake, fake, fake, fake, 0, 4, 8, 8, 64, 64, 512, 512, 512, 512,
-                              1, 0.1, 1, 1, None)
+                              1, 0.1, 1, 1, 0, None, 0, None)
     assert rc == _lib.TV_EINVAL and b"empty" in lib.tv_last_error()
     rc = lib.tv_read_kv_blocks(fake, fake, fake, fake, fake, 1, 17, 4, 64, 16, 10, 1, None)
     assert rc == _lib.TV_EINVAL and b"exceeds" in lib.tv_last_error()
@@ -85,3 +89,16 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(ImportError, match="no fallback"):
         _lib.load()
+
+
+def test_no_bit_cast_of_vector_element_lvalues():
+    """hipcc (ROCm 7.2) reads element 0 when __builtin_bit_cast is applied to an
+    element of an ext_vector_type lvalue (v[i]); sources must go through a
+    by-value helper such as u32_as_f32 instead."""
+    csrc = Path(__file__).resolve().parents[1] / "tinyvllm_amd" / "csrc"
+    bad = []
+    for f in sorted(csrc.glob("*")):
+        for n, line in enumerate(f.read_text().splitlines(), 1):
+            if re.search(r"__builtin_bit_cast\(\s*\w+\s*,\s*\w+(\[[^\]]*\])+\s*\)", line):
+                bad.append(f"{f.name}:{n}: {line.strip()}")
+    assert not bad, "\n".join(bad)

@@ -143,3 +143,15 @@ def test_rejects_batch_above_one():
     q = randn(47, 2, 8, 4, 32).cuda()
     with pytest.raises(ValueError, match="batch 1"):
         _op()(q, q[:, :, :4], q[:, :, :4], True)
+
+
+@pytest.mark.parametrize("chunk_tiles", [1, 2, 3, 5])
+@pytest.mark.parametrize("lq,causal", [(130, True), (500, True), (200, False)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_mfma_split_rows_merge(chunk_tiles, lq, causal, dtype):
+    """Long rows split into key chunks on separate work-groups, merged by a second kernel."""
+    q, k, v = (randn(60 + i, lq, 8 if i == 0 else 2, 64, dtype=dtype) for i in range(3))
+    out = _op()(q.unsqueeze(0).cuda(), k.unsqueeze(0).cuda(), v.unsqueeze(0).cuda(), causal,
+                chunk_tiles=chunk_tiles)[0]
+    want = flash_prefill_ref(q.float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None], causal)[0]
+    assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-2

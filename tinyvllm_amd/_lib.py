@@ -25,12 +25,14 @@ SIGNATURES = {
     "tv_last_error": (ctypes.c_char_p, []),
     "tv_paged_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),
     "tv_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P, _S, _P]),
-    "tv_flash_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _L, _I, _F, _I, _I, _P]),
+    "tv_flash_prefill_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I, _I]),
+    "tv_flash_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _L, _I, _F, _I, _I,
+                              _I, _P, _S, _P]),
     "tv_reshape_and_cache": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _L, _L, _I, _P, _P]),
     "tv_write_kv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _L, _L, _I, _P]),
     "tv_read_kv_blocks": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 

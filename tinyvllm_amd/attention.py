@@ -110,11 +110,13 @@ def _token_rows(t, name):
     return t.stride(1)
 
 
-def flash_prefill_attention(queries, keys, values, causal=True, *, out_dtype=None):
+def flash_prefill_attention(queries, keys, values, causal=True, *, out_dtype=None, chunk_tiles=0):
     """Prefill attention over one prompt (tinyvllm/model/llama.py:58-94).
 
     queries [1,Lq,Hq,D], keys [1,Lk,Hkv,D], values [1,Lk,Hkv,Dv] -> [1,Lq,Hq,Dv].
     ``causal`` masks key j for query i when j > i (top-left aligned).
+    ``chunk_tiles`` (keyword-only, not in the reference): 64-key tiles per work
+    unit when long causal rows are split; 0 picks it from the shape.
     """
     lib = _lib.load()
     dev = _on_gpu(queries, keys, values)
@@ -130,11 +132,14 @@ def flash_prefill_attention(queries, keys, values, causal=True, *, out_dtype=Non
     dv = values.shape[3]
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     out = torch.empty((1, lq, hq, dv), dtype=out_dtype, device=dev)
+    code = _lib.dtype_code(queries.dtype)
+    ws_bytes = lib.tv_flash_prefill_workspace_bytes(lq, lk, hq, d, dv, 1 if causal else 0, code, chunk_tiles)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.tv_flash_prefill(
         out.data_ptr(), queries.data_ptr(), keys.data_ptr(), values.data_ptr(),
         lq, lk, hq, hkv, d, dv, qs, ks, vs, hq * dv, 1 if causal else 0,
-        1.0 / math.sqrt(d), _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype),
-        _lib.stream_ptr(dev))
+        1.0 / math.sqrt(d), code, _lib.dtype_code(out_dtype), chunk_tiles,
+        ws.data_ptr() if ws is not None else None, ws_bytes, _lib.stream_ptr(dev))
     _lib.check(rc, "flash_prefill_attention")
     return out
 
@@ -186,7 +191,7 @@ class PagedDecodePlan:
 class PrefillPlan:
     """Pre-validated, pointer-stable causal prefill for fixed [1, L, H, D] inputs."""
 
-    def __init__(self, queries, keys, values, causal=True, *, out_dtype=None):
+    def __init__(self, queries, keys, values, causal=True, *, out_dtype=None, chunk_tiles=0):
         self.lib = _lib.load()
         self.dev = _on_gpu(queries, keys, values)
         qs, ks, vs = _token_rows(queries, "queries"), _token_rows(keys, "keys"), _token_rows(values, "values")
@@ -194,11 +199,15 @@ class PrefillPlan:
         _, lk, hkv, _ = keys.shape
         dv = values.shape[3]
         out_dtype = queries.dtype if out_dtype is None else out_dtype
+        code = _lib.dtype_code(queries.dtype)
         self.out = torch.empty((1, lq, hq, dv), dtype=out_dtype, device=self.dev)
+        self.ws_bytes = self.lib.tv_flash_prefill_workspace_bytes(lq, lk, hq, d, dv, 1 if causal else 0, code,
+                                                                  chunk_tiles)
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=self.dev)
         self._inputs = (queries, keys, values)
         self.args = (self.out.data_ptr(), queries.data_ptr(), keys.data_ptr(), values.data_ptr(),
                      lq, lk, hq, hkv, d, dv, qs, ks, vs, hq * dv, 1 if causal else 0, 1.0 / math.sqrt(d),
-                     _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype))
+                     code, _lib.dtype_code(out_dtype), chunk_tiles, self.ws.data_ptr(), self.ws_bytes)
 
     def run(self):
         _lib.check(self.lib.tv_flash_prefill(*self.args, _lib.stream_ptr(self.dev)), "PrefillPlan.run")

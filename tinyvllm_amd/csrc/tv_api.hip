@@ -2,6 +2,7 @@
 // Host-side validation lives here; kernels assume validated arguments.
 #include <cstdio>
 #include <cstdarg>
+#include <algorithm>
 #include <initializer_list>
 #include <string>
 
@@ -65,7 +66,7 @@ int vec_width(std::initializer_list<long long> sizes, std::initializer_list<cons
 
 extern "C" {
 
-int tv_abi_version(void) { return 1; }
+int tv_abi_version(void) { return 2; }
 
 const char* tv_last_error(void) { return g_err.c_str(); }
 
@@ -160,25 +161,11 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   return check_launch("tv_paged_decode(merge)");
 }
 
-int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int q_len, int kv_len, int num_heads,
-                     int num_kv_heads, int head_dim, int head_dim_v, int64_t q_stride, int64_t k_stride,
-                     int64_t v_stride, int64_t out_stride, int causal, float scale, int dtype, int out_dtype,
-                     void* stream) {
-  if (!out || !q || !k || !v) return fail(TV_EINVAL, "tv_flash_prefill: null pointer argument");
-  if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
-    return fail(TV_EINVAL, "tv_flash_prefill: bad dtype %d / out_dtype %d", dtype, out_dtype);
-  if (q_len <= 0 || kv_len <= 0)
-    return fail(TV_EINVAL, "tv_flash_prefill: empty sequence (q_len=%d, kv_len=%d)", q_len, kv_len);
-  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
-    return fail(TV_EINVAL, "tv_flash_prefill: bad head counts (%d, %d)", num_heads, num_kv_heads);
-  if (head_dim <= 0 || head_dim_v <= 0)
-    return fail(TV_EINVAL, "tv_flash_prefill: bad head dims (%d, %d)", head_dim, head_dim_v);
-  if (q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim ||
-      v_stride < (int64_t)num_kv_heads * head_dim_v || out_stride < (int64_t)num_heads * head_dim_v)
-    return fail(TV_EINVAL, "tv_flash_prefill: token stride smaller than a token row");
-  if (q_len > 65535 * 64 || num_heads > 65535)
-    return fail(TV_EINVAL, "tv_flash_prefill: grid too large");
-  tv::PrefillParams p{};
+static void prefill_params(tv::PrefillParams& p, void* out, const void* q, const void* k, const void* v, int q_len,
+                           int kv_len, int num_heads, int num_kv_heads, int head_dim, int head_dim_v,
+                           int64_t q_stride, int64_t k_stride, int64_t v_stride, int64_t out_stride, int causal,
+                           float scale, int out_dtype, int chunk_tiles) {
+  p = tv::PrefillParams{};
   p.out = out;
   p.q = q;
   p.k = k;
@@ -196,8 +183,55 @@ int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int
   p.causal = causal ? 1 : 0;
   p.scale = scale;
   p.out_dtype = out_dtype;
-  if (tv::launch_flash_prefill(p, dtype, true, reinterpret_cast<hipStream_t>(stream)) != 0)
+  if (chunk_tiles <= 0) {
+    // Default: no split.  Splitting a causal row across work-groups writes an
+    // fp32 partial of the whole query tile per chunk and reads it back in a
+    // merge kernel; on MI355X that round trip cost more than the shorter chains
+    // saved at every chunk size tried (L = 512 / 1024, 32 heads, head_dim 64).
+    chunk_tiles = (kv_len + 63) / 64;
+  }
+  p.chunk_tiles = chunk_tiles;
+}
+
+size_t tv_flash_prefill_workspace_bytes(int q_len, int kv_len, int num_heads, int head_dim, int head_dim_v,
+                                        int causal, int dtype, int chunk_tiles) {
+  if (q_len <= 0 || kv_len <= 0 || num_heads <= 0 || head_dim <= 0 || head_dim_v <= 0 || !valid_dtype(dtype))
+    return 0;
+  tv::PrefillParams p;
+  // dense strides and aligned placeholder addresses: the size assumes the MFMA path
+  prefill_params(p, nullptr, (void*)256, (void*)256, (void*)256, q_len, kv_len, num_heads, 1, head_dim, head_dim_v,
+                 (int64_t)num_heads * head_dim, head_dim, head_dim_v, (int64_t)num_heads * head_dim_v, causal, 1.0f,
+                 dtype, chunk_tiles);
+  return tv::prefill_workspace_bytes(p, dtype);
+}
+
+int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int q_len, int kv_len, int num_heads,
+                     int num_kv_heads, int head_dim, int head_dim_v, int64_t q_stride, int64_t k_stride,
+                     int64_t v_stride, int64_t out_stride, int causal, float scale, int dtype, int out_dtype,
+                     int chunk_tiles, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!out || !q || !k || !v) return fail(TV_EINVAL, "tv_flash_prefill: null pointer argument");
+  if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
+    return fail(TV_EINVAL, "tv_flash_prefill: bad dtype %d / out_dtype %d", dtype, out_dtype);
+  if (q_len <= 0 || kv_len <= 0)
+    return fail(TV_EINVAL, "tv_flash_prefill: empty sequence (q_len=%d, kv_len=%d)", q_len, kv_len);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(TV_EINVAL, "tv_flash_prefill: bad head counts (%d, %d)", num_heads, num_kv_heads);
+  if (head_dim <= 0 || head_dim_v <= 0)
+    return fail(TV_EINVAL, "tv_flash_prefill: bad head dims (%d, %d)", head_dim, head_dim_v);
+  if (q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim ||
+      v_stride < (int64_t)num_kv_heads * head_dim_v || out_stride < (int64_t)num_heads * head_dim_v)
+    return fail(TV_EINVAL, "tv_flash_prefill: token stride smaller than a token row");
+  if (q_len > 65535 * 64 || num_heads > 65535)
+    return fail(TV_EINVAL, "tv_flash_prefill: grid too large");
+  tv::PrefillParams p;
+  prefill_params(p, out, q, k, v, q_len, kv_len, num_heads, num_kv_heads, head_dim, head_dim_v, q_stride, k_stride,
+                 v_stride, out_stride, causal, scale, out_dtype, chunk_tiles);
+  const int rc = tv::launch_flash_prefill(p, dtype, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  if (rc == 1)
     return fail(TV_EUNSUPPORTED, "tv_flash_prefill: head_dim %d / %d not supported (max 256)", head_dim, head_dim_v);
+  if (rc == 2)
+    return fail(TV_EINVAL, "tv_flash_prefill: workspace of %zu bytes required (got %zu)",
+                tv::prefill_workspace_bytes(p, dtype), workspace_bytes);
   return check_launch("tv_flash_prefill");
 }
 

@@ -25,6 +25,10 @@ struct PrefillParams {
   float scale;
   int out_dtype;
   int xcd_remap;         // 1: place the heads of a KV group on one XCD
+  int chunk_tiles;       // key tiles per work unit (long causal rows are split)
+  int max_chunks;        // largest number of key chunks of one query tile
+  float* part_o;         // [Hq, nqt, max_chunks, 64, head_dim] chunk outputs (split tiles only)
+  float* part_ml;        // [Hq, nqt, max_chunks, 64, 2] chunk (max, sum)
 };
 
 // Cache write from a slot mapping or a base slot (kv_cache.hip).
@@ -56,7 +60,10 @@ struct KVGatherParams {
   int num_blocks;
 };
 
-int launch_flash_prefill(const PrefillParams& p, int dtype, bool allow_mfma, hipStream_t stream);
+bool prefill_uses_mfma(const PrefillParams& p, int dtype);
+size_t prefill_workspace_bytes(const PrefillParams& p, int dtype);
+int launch_flash_prefill(const PrefillParams& p, int dtype, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 void launch_kv_write(const KVWriteParams& p, int vec_bytes, hipStream_t stream);
 void launch_kv_gather(const KVGatherParams& p, int vec_bytes, hipStream_t stream);
 
