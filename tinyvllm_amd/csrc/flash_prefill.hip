@@ -70,7 +70,13 @@ __device__ __forceinline__ int prefill_head(int x, int num_heads, int remap) {
 }
 
 constexpr int kPrefillBM = 64;   // query rows per work unit (16 per wave)
-constexpr int kPrefillBN = 64;   // keys per tile
+#ifndef TV_PREFILL_BN
+#define TV_PREFILL_BN 64
+#endif
+constexpr int kPrefillBN = TV_PREFILL_BN;   // keys per tile (64 or 128)
+#ifndef TV_PREFILL_KSPLIT
+#define TV_PREFILL_KSPLIT 2   // groups of 4 waves splitting a row block's key tiles (head_dim 64)
+#endif
 
 // Key tiles query tile qt needs (causal rows stop at the diagonal).
 __device__ __forceinline__ int prefill_key_tiles(const PrefillParams& p, int qt) {
@@ -90,20 +96,46 @@ __device__ __forceinline__ void prefill_unit(const PrefillParams& p, int u, int&
   chunk = u;
 }
 
-template <typename T, int D>
-__global__ void __launch_bounds__(256) prefill_mfma_kernel(const PrefillParams p) {
+// Store 4 consecutive output elements (a row slice of one query) as out_dtype.
+template <typename T>
+__device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v, int out_dtype) {
+  if (out_dtype == kF32) {
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(base) + idx) = v;
+  } else {
+    const u32x2 w = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(base) + idx) = w;
+  }
+}
+
+// KSPLIT groups of 4 waves share the 64 query rows of a work-group; group s
+// takes key tiles kt0 + s, kt0 + s + KSPLIT, ... in its own LDS buffers and the
+// groups merge their (max, row sum, O) through LDS at the end.  Every group
+// runs the same number of steps (idle groups load and skip a clamped tile) so
+// all waves meet at every barrier.
+template <typename T, int D, int KSPLIT>
+__global__ void __launch_bounds__(256 * KSPLIT) prefill_mfma_kernel(const PrefillParams p) {
   constexpr int BM = kPrefillBM;
   constexpr int BN = kPrefillBN;
   constexpr int KP = D + 8;       // LDS pitch of the K tile (elements)
-  constexpr int VP = BN + 8;      // LDS pitch of the V^T tile (elements)
-  constexpr int DB = D / 16;      // 16-row blocks of O^T
+  constexpr int VP = BN + 4;      // LDS pitch of the V^T tile: 8-byte reads of 16 rows hit distinct banks
+  constexpr int DB = D / 16;      // 16-row blocks of O^T; block DB holds the row sums
   constexpr int KS = D / 32;      // MFMA steps over the head dim
-  constexpr int VPT = BN * (D / 8) / 256;   // 16-byte vectors of K (and of V) per thread per tile
-  __shared__ __attribute__((aligned(16))) uint16_t sk[BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sv[D * VP];
+  constexpr int VPT = BN * (D / 8) / 256;          // 16-byte K vectors per thread per tile
+  constexpr int VPT2 = (BN / 2) * (D / 8) / 256;   // V key pairs per thread per tile
+  constexpr int SK = BN * KP;                // K tile (elements)
+  constexpr int SV = (D + 16) * VP;          // V^T tile plus 16 rows of ones
+  // V^T tile plus 16 rows of ones: the MFMA against them yields the softmax
+  // row sums of the (rounded) P that the numerator uses, for free.
+  // tile buffers of all groups; reused afterwards for the group merge
+  constexpr int TILE_ELEMS = KSPLIT * (SK + SV);
+  constexpr int MERGE_ELEMS = KSPLIT > 1 ? KSPLIT * (BM * (D + 16) + BM) * 2 : 0;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[TILE_ELEMS > MERGE_ELEMS ? TILE_ELEMS : MERGE_ELEMS];
 
-  const int tid = threadIdx.x;
+  const int grp = threadIdx.x >> 8;          // key-split group
+  const int tid = threadIdx.x & 255;         // thread within the group
   const int wave = tid >> 6;
+  uint16_t* sk = smem + grp * (SK + SV);
+  uint16_t* sv = sk + SK;
   const int lane = tid & 63;
   const int g = lane >> 4;        // 0..3
   const int col = lane & 15;
@@ -123,65 +155,100 @@ __global__ void __launch_bounds__(256) prefill_mfma_kernel(const PrefillParams p
 
   u32x4 qf[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    if (qi < p.q_len)
-      qf[ks] = *reinterpret_cast<const u32x4*>(qg + (size_t)qi * p.q_stride + (size_t)h * D + ks * 32 + g * 8);
-    else
-      qf[ks] = u32x4{0, 0, 0, 0};
+  for (int ks = 0; ks < KS; ++ks)
+    qf[ks] = qi < p.q_len
+                 ? *reinterpret_cast<const u32x4*>(qg + (size_t)qi * p.q_stride + (size_t)h * D + ks * 32 + g * 8)
+                 : u32x4{0, 0, 0, 0};
+
+  {  // ones rows of the extended V^T (never overwritten by tile stores)
+    const uint16_t one = __builtin_bit_cast(uint16_t, from_float<T>(1.0f));
+    for (int idx = tid; idx < 16 * VP; idx += 256) sv[D * VP + idx] = one;
   }
 
-  // next tile's K and V, fetched into registers while the current tile computes
-  u32x4 kpre[VPT], vpre[VPT];
-  auto gload = [&](int kt) {
-    const int k0 = kt * BN;
+  // Per-thread element offsets inside a tile (the tile base is wave-uniform).
+  // K: thread -> (key, 8-dim chunk), consecutive lanes along a row.
+  // V: thread -> (key pair, 8-dim chunk); pairs are interleaved into 32-bit
+  //    words with v_perm so V^T is written with ds_write_b32.
+  int k_row[VPT], k_col[VPT], v_row[VPT2], v_col[VPT2];
+  size_t k_off[VPT], v_off[VPT2];   // element offsets from the tile's first row (full tiles)
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int idx = tid + i * 256;
-      const int kk = idx / (D / 8);                  // K: consecutive lanes walk a row
-      const int kc = idx - kk * (D / 8);
-      kpre[i] = k0 + kk < p.kv_len
-                    ? *reinterpret_cast<const u32x4*>(kg + (size_t)(k0 + kk) * p.k_stride + kc * 8)
-                    : u32x4{0, 0, 0, 0};
-      const int vk = idx % BN;                       // V: consecutive lanes walk keys
-      const int vc = idx / BN;
-      vpre[i] = k0 + vk < p.kv_len
-                    ? *reinterpret_cast<const u32x4*>(vg + (size_t)(k0 + vk) * p.v_stride + vc * 8)
-                    : u32x4{0, 0, 0, 0};
+  for (int i = 0; i < VPT; ++i) {
+    const int idx = tid + i * 256;
+    k_row[i] = idx / (D / 8);
+    k_col[i] = idx - k_row[i] * (D / 8);
+    k_off[i] = (size_t)k_row[i] * p.k_stride + k_col[i] * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < VPT2; ++i) {
+    const int unit = tid + i * 256;
+    v_row[i] = 2 * (unit % (BN / 2));
+    v_col[i] = unit / (BN / 2);
+    v_off[i] = (size_t)v_row[i] * p.v_stride + v_col[i] * 8;
+  }
+
+  struct TileRegs {
+    u32x4 k[VPT];
+    u32x4 v[VPT2][2];
+    int k0;   // first key of the tile
+  };
+  // Every step issues the same loads (rows past kv_len re-read the last valid
+  // row), so the compiler waits for exactly the tile it needs; the registers
+  // are not touched until lstore.
+  auto gload = [&](int kt, TileRegs& r) {
+    const int k0 = kt * BN;
+    r.k0 = k0;
+    const T* kb = kg + (size_t)k0 * p.k_stride;
+    const T* vb = vg + (size_t)k0 * p.v_stride;
+    if (k0 + BN <= p.kv_len) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) r.k[i] = *reinterpret_cast<const u32x4*>(kb + k_off[i]);
+#pragma unroll
+      for (int i = 0; i < VPT2; ++i) {
+        r.v[i][0] = *reinterpret_cast<const u32x4*>(vb + v_off[i]);
+        r.v[i][1] = *reinterpret_cast<const u32x4*>(vb + v_off[i] + p.v_stride);
+      }
+    } else {
+      const int last = p.kv_len - 1 - k0;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        r.k[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)min(k_row[i], last) * p.k_stride + k_col[i] * 8);
+#pragma unroll
+      for (int i = 0; i < VPT2; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          r.v[i][t] = *reinterpret_cast<const u32x4*>(vb + (size_t)min(v_row[i] + t, last) * p.v_stride +
+                                                       v_col[i] * 8);
     }
   };
-  auto lstore = [&]() {
+  auto lstore = [&](const TileRegs& r) {
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int idx = tid + i * 256;
-      const int kk = idx / (D / 8);
-      const int kc = idx - kk * (D / 8);
-      *reinterpret_cast<u32x4*>(&sk[kk * KP + kc * 8]) = kpre[i];
-      const int vk = idx % BN;
-      const int vc = idx / BN;
+    for (int i = 0; i < VPT; ++i) *reinterpret_cast<u32x4*>(&sk[k_row[i] * KP + k_col[i] * 8]) = r.k[i];
+    const bool partial = r.k0 + BN > p.kv_len;   // zero V rows past the sequence
+#pragma unroll
+    for (int i = 0; i < VPT2; ++i) {
+      u32x4 v0 = r.v[i][0], v1 = r.v[i][1];
+      if (partial) {
+        if (r.k0 + v_row[i] >= p.kv_len) v0 = u32x4{0, 0, 0, 0};
+        if (r.k0 + v_row[i] + 1 >= p.kv_len) v1 = u32x4{0, 0, 0, 0};
+      }
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        sv[(vc * 8 + 2 * w) * VP + vk] = (uint16_t)(vpre[i][w] & 0xffffu);
-        sv[(vc * 8 + 2 * w + 1) * VP + vk] = (uint16_t)(vpre[i][w] >> 16);
+        uint16_t* dst = &sv[(v_col[i] * 8 + 2 * w) * VP + v_row[i]];
+        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(dst + VP) = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
       }
     }
   };
 
-  f32x4 oacc[DB];
+  f32x4 oacc[DB + 1];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = kNegInf;
-  float lsum = 0.0f;
+  for (int i = 0; i <= DB; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = kNegInf;      // running max of the raw scores q.k of this query column
   const float c = p.scale * kLog2e;
 
-  if (kt0 < kt1) gload(kt0);
-  for (int kt = kt0; kt < kt1; ++kt) {
+  auto compute = [&](int kt) {
     const int k0 = kt * BN;
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (kt + 1 < kt1) gload(kt + 1);
-
-    // S^T = K Q^T for four 16-key blocks: st[kb][i] = S[q = qi][key = k0 + kb*16 + 4g + i]
+    // S^T = K Q^T: st[kb][i] = q.k for query qi and key k0 + kb*16 + 4g + i
     f32x4 st[BN / 16];
 #pragma unroll
     for (int kb = 0; kb < BN / 16; ++kb) {
@@ -192,80 +259,130 @@ __global__ void __launch_bounds__(256) prefill_mfma_kernel(const PrefillParams p
         st[kb] = mfma16x16x32<T>(a, qf[ks], st[kb]);
       }
     }
-
-    // scale (log2 domain) and mask; tiles fully below the diagonal need no mask
-    const bool full = k0 + BN <= p.kv_len && (!p.causal || k0 + BN - 1 <= qt * BM);
-    float mt = kNegInf;
+    // mask only tiles that cross the diagonal or the end of the sequence
+    if (!(k0 + BN <= p.kv_len && (!p.causal || k0 + BN - 1 <= qt * BM))) {
+      const int lim = p.causal ? min(p.kv_len - 1, qi) : p.kv_len - 1;   // last visible key
 #pragma unroll
-    for (int kb = 0; kb < BN / 16; ++kb) {
+      for (int kb = 0; kb < BN / 16; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = st[kb][i] * c;
-        if (!full) {
-          const int kidx = k0 + kb * 16 + 4 * g + i;
-          const bool ok = kidx < p.kv_len && (!p.causal || kidx <= qi);
-          x = ok ? x : kNegInf;
-        }
-        st[kb][i] = x;
-        mt = fmaxf(mt, x);
-      }
+        for (int i = 0; i < 4; ++i) st[kb][i] = k0 + kb * 16 + 4 * g + i <= lim ? st[kb][i] : kNegInf;
+    }
+    float mt;
+    {  // max of the 4*BN/16 raw scores with a v_max3 tree
+      float r[BN / 16 * 4];
+#pragma unroll
+      for (int kb = 0; kb < BN / 16; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[kb * 4 + i] = st[kb][i];
+      constexpr int N = BN / 16 * 4;
+      float t[(N + 2) / 3];
+#pragma unroll
+      for (int a = 0; a < N / 3; ++a) t[a] = fmaxf(fmaxf(r[3 * a], r[3 * a + 1]), r[3 * a + 2]);
+      int nt = N / 3;
+      if constexpr (N % 3 == 1) t[nt++] = r[N - 1];
+      if constexpr (N % 3 == 2) t[nt++] = fmaxf(r[N - 2], r[N - 1]);
+      mt = t[0];
+#pragma unroll
+      for (int a = 1; a + 1 < (N + 2) / 3; a += 2) mt = fmaxf(fmaxf(mt, t[a]), t[a + 1]);
+      if constexpr (((N + 2) / 3) % 2 == 0) mt = fmaxf(mt, t[(N + 2) / 3 - 1]);
     }
     mt = max_over_g(mt);
-    // raise the running max only when it grows by more than the slack (rare
-    // after the first tile); weights stay <= 2^8
-    if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f) != 0) {
+    // the running max is only raised when it grows by more than 8 log2 units
+    // (rare after the first tile); unnormalised weights stay <= 2^8
+    const float mtc = mt * c;
+    float mc = m == kNegInf ? kNegInf : m * c;
+    if (__builtin_amdgcn_ballot_w64(mtc > mc + 8.0f) != 0) {
       __asm__ volatile("" ::: "memory");
-      const float mn = mt > m + 8.0f ? fmaxf(m, mt) : m;
-      const float alpha = mn == kNegInf ? 1.0f : fast_exp2(m - mn);
+      const float mn = mtc > mc + 8.0f ? fmaxf(m, mt) : m;
+      const float alpha = mn == kNegInf ? 1.0f : fast_exp2((m - mn) * c);
       m = mn;
-      lsum *= alpha;
+      mc = m == kNegInf ? kNegInf : m * c;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+      for (int db = 0; db <= DB; ++db) oacc[db] *= alpha;
     }
-    const float mu = m == kNegInf ? 0.0f : m;
-#pragma unroll
-    for (int kb = 0; kb < BN / 16; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = fast_exp2(st[kb][i] - mu);
-        st[kb][i] = e;
-        lsum += e;
-      }
-
-    // P^T fragments: reduction index kk = 8g + j maps to key 4g+j (j<4) of block
-    // 2*ks2 and key 4g+j-4 (j>=4) of block 2*ks2+1.
+    if (mc == kNegInf) mc = 0.0f;
     u32x4 pf[BN / 32];
 #pragma unroll
-    for (int ks2 = 0; ks2 < BN / 32; ++ks2) {
-      pf[ks2][0] = pack2<T>(st[2 * ks2][0], st[2 * ks2][1]);
-      pf[ks2][1] = pack2<T>(st[2 * ks2][2], st[2 * ks2][3]);
-      pf[ks2][2] = pack2<T>(st[2 * ks2 + 1][0], st[2 * ks2 + 1][1]);
-      pf[ks2][3] = pack2<T>(st[2 * ks2 + 1][2], st[2 * ks2 + 1][3]);
+    for (int kb = 0; kb < BN / 16; ++kb) {
+      const float e0 = fast_exp2(fmaf(st[kb][0], c, -mc));
+      const float e1 = fast_exp2(fmaf(st[kb][1], c, -mc));
+      const float e2 = fast_exp2(fmaf(st[kb][2], c, -mc));
+      const float e3 = fast_exp2(fmaf(st[kb][3], c, -mc));
+      // reduction index kk = 8g + j maps to key 4g+j (j<4) of block 2*ks2 and
+      // key 4g+j-4 (j>=4) of block 2*ks2+1 on both MFMA operands
+      pf[kb >> 1][(kb & 1) * 2] = pack2<T>(e0, e1);
+      pf[kb >> 1][(kb & 1) * 2 + 1] = pack2<T>(e2, e3);
     }
-    // O^T += V^T P^T: oacc[db][i] = O[q = qi][d = db*16 + 4g + i]
+    // O^T += V^T P^T (block DB: the ones rows -> row sums)
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    for (int db = 0; db <= DB; ++db) {
 #pragma unroll
       for (int ks2 = 0; ks2 < BN / 32; ++ks2) {
         const uint16_t* row = &sv[(db * 16 + col) * VP + ks2 * 32 + 4 * g];
         const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
-        const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        oacc[db] = mfma16x16x32<T>(a, pf[ks2], oacc[db]);
+        oacc[db] = mfma16x16x32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf[ks2], oacc[db]);
       }
     }
+  };
+  // group tile sequence: kt0 + grp + KSPLIT * j, j < nsteps (same count for all groups)
+  const int nsteps = (kt1 - kt0 + KSPLIT - 1) / KSPLIT;
+  auto tile_of = [&](int j) { return min(kt0 + grp + KSPLIT * j, kt1 - 1); };
+  auto step = [&](int j, TileRegs& r) {
+    lds_barrier();
+    lstore(r);
+    lds_barrier();
+    gload(tile_of(j + 2), r);          // two steps ahead (clamped: re-reads are unused)
+    if (kt0 + grp + KSPLIT * j < kt1) compute(kt0 + grp + KSPLIT * j);
+  };
+
+  TileRegs ra, rb;
+  gload(tile_of(0), ra);
+  gload(tile_of(1), rb);
+  // both steps of the loop body are unconditional so the number of loads in
+  // flight is the same on every path (the final odd step is peeled)
+  int j = 0;
+  for (; j + 1 < nsteps; j += 2) {
+    step(j, ra);
+    step(j + 1, rb);
+  }
+  if (j < nsteps) step(j, ra);
+
+  if constexpr (KSPLIT > 1) {
+    // merge the groups: each publishes (scaled max, O unnormalised incl. row sums)
+    lds_barrier();
+    float* so = reinterpret_cast<float*>(smem);                  // [KSPLIT][64 rows][D + 16]
+    float* sm = so + KSPLIT * BM * (D + 16);                     // [KSPLIT][64 rows]
+    const int row = wave * 16 + col;
+#pragma unroll
+    for (int db = 0; db <= DB; ++db)
+      *reinterpret_cast<f32x4*>(&so[(grp * BM + row) * (D + 16) + db * 16 + 4 * g]) = oacc[db];
+    if (g == 0) sm[grp * BM + row] = m == kNegInf ? kNegInf : m * c;
+    lds_barrier();
+    if (grp != 0) return;
+    float M = kNegInf;
+#pragma unroll
+    for (int s2 = 0; s2 < KSPLIT; ++s2) M = fmaxf(M, sm[s2 * BM + row]);
+#pragma unroll
+    for (int db = 0; db <= DB; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < KSPLIT; ++s2) {
+      const float ms = sm[s2 * BM + row];
+      const float f = ms == kNegInf ? 0.0f : fast_exp2(ms - M);
+#pragma unroll
+      for (int db = 0; db <= DB; ++db)
+        oacc[db] += *reinterpret_cast<const f32x4*>(&so[(s2 * BM + row) * (D + 16) + db * 16 + 4 * g]) * f;
+    }
+    m = M == kNegInf ? kNegInf : M / c;
   }
 
-  lsum = sum_over_g(lsum);
+  const float lsum = oacc[DB][0];
   if (qi >= p.q_len) return;
+  const float inv = 1.0f / lsum;
   if (nchunks == 1) {
-    const float inv = 1.0f / lsum;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        store_as(p.out, (size_t)qi * p.out_stride + (size_t)h * D + db * 16 + 4 * g + i, oacc[db][i] * inv,
-                 p.out_dtype);
+      store4<T>(p.out, (size_t)qi * p.out_stride + (size_t)h * D + db * 16 + 4 * g, oacc[db] * inv, p.out_dtype);
     return;
   }
   // partial of this key chunk: normalised O plus (max, sum) per query row
@@ -273,12 +390,10 @@ __global__ void __launch_bounds__(256) prefill_mfma_kernel(const PrefillParams p
   const size_t unit = ((size_t)h * nqt + qt) * p.max_chunks + chunk;
   const int row = qi - qt * BM;
   float* po = p.part_o + (unit * BM + row) * D;
-  const float inv = 1.0f / lsum;
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
-    *reinterpret_cast<f32x4*>(po + db * 16 + 4 * g) = oacc[db] * inv;
+  for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(po + db * 16 + 4 * g) = oacc[db] * inv;
   if (g == 0) {
-    p.part_ml[(unit * BM + row) * 2] = m;
+    p.part_ml[(unit * BM + row) * 2] = m == kNegInf ? kNegInf : m * c;
     p.part_ml[(unit * BM + row) * 2 + 1] = lsum;
   }
 }
@@ -427,14 +542,16 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
       pp.part_o = reinterpret_cast<float*>(workspace);
       pp.part_ml = pp.part_o + (size_t)pp.num_heads * nqt * max_chunks * kPrefillBM * pp.head_dim;
     }
-    const dim3 grid(pp.num_heads, units);
     const bool d64 = pp.head_dim == 64;
+    const dim3 grid(pp.num_heads, units);
+    constexpr int KSP = TV_PREFILL_KSPLIT;
+    const dim3 block(256 * KSP);
     if (dtype == kF16) {
-      if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 64>), grid, dim3(256), 0, stream, pp);
-      else hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128>), grid, dim3(256), 0, stream, pp);
+      if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 64, KSP>), grid, block, 0, stream, pp);
+      else hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128, 1>), grid, dim3(256), 0, stream, pp);
     } else {
-      if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 64>), grid, dim3(256), 0, stream, pp);
-      else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128>), grid, dim3(256), 0, stream, pp);
+      if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 64, KSP>), grid, block, 0, stream, pp);
+      else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
     }
     if (max_chunks > 1) {
       const dim3 mgrid(pp.num_heads, (pp.q_len + kPrefillBM - 1) / kPrefillBM);

@@ -188,7 +188,7 @@ static void prefill_params(tv::PrefillParams& p, void* out, const void* q, const
     // fp32 partial of the whole query tile per chunk and reads it back in a
     // merge kernel; on MI355X that round trip cost more than the shorter chains
     // saved at every chunk size tried (L = 512 / 1024, 32 heads, head_dim 64).
-    chunk_tiles = (kv_len + 63) / 64;
+    chunk_tiles = kv_len;   // >= the number of key tiles of any size
   }
   p.chunk_tiles = chunk_tiles;
 }

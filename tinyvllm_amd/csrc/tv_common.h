@@ -138,4 +138,13 @@ template <int N> __device__ __forceinline__ float group_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Work-group barrier that orders LDS traffic only.  __syncthreads() also fences
+// global memory, which makes every wave wait for all of its outstanding global
+// loads (vmcnt(0)) -- including loads issued ahead as prefetch.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace tv
