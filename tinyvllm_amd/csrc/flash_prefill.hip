@@ -84,9 +84,20 @@ __device__ __forceinline__ int prefill_key_tiles(const PrefillParams& p, int qt)
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
-// Map grid.y (longest work first) to (query tile, chunk of key tiles).
+// Map grid.y to (query tile, chunk of key tiles).  Without chunk splitting
+// the order is zig-zag: the longer half of the causal query tiles longest
+// first, then the shorter half shortest first, so the two work-groups that
+// become resident on one CU (linear ids i and i + grid/2) carry about the
+// same total number of key tiles.  With splitting: longest first.
 __device__ __forceinline__ void prefill_unit(const PrefillParams& p, int u, int& qt, int& chunk, int& nchunks) {
   const int nqt = (p.q_len + kPrefillBM - 1) / kPrefillBM;
+  if (p.max_chunks == 1) {
+    const int half = (nqt + 1) / 2;
+    qt = u < half ? nqt - 1 - u : u - half;
+    chunk = 0;
+    nchunks = 1;
+    return;
+  }
   for (qt = nqt - 1; qt > 0; --qt) {
     const int ch = (prefill_key_tiles(p, qt) + p.chunk_tiles - 1) / p.chunk_tiles;
     if (u < ch) break;
