@@ -1,0 +1,161 @@
+"""numpy restatement of the reference's LLaMA forward passes (test infrastructure).
+
+Follows tinyvllm/model/llama.py step by step:
+
+* ``rms_norm_ref``      RMSNorm.__call__, llama.py:14-23: x * rsqrt(mean(x^2) + eps) * w
+* ``rope_tables_ref``   precompute_freqs_cis, llama.py:26-31 (float32, as tinygrad's .float())
+* ``apply_rope_ref``    apply_rope, llama.py:34-55: interleaved pairs (2i, 2i+1)
+* ``silu_ref``          Tensor.silu = x * sigmoid(x), used by FeedForward, llama.py:220-221
+* ``LlamaRef.prefill``  Llama.prefill + TransformerBlock + Attention, llama.py:147-285:
+                        K/V written to the cache, attention over this chunk only (llama.py:184)
+* ``LlamaRef.decode``   Llama.create_jit_decode + Llama.decode, llama.py:290-388:
+                        ``write_before_attend=False`` is the reference's order (attention
+                        first, K/V written at get_slot() afterwards, llama.py:378-386);
+                        True writes first (the order of the HIP step's default)
+* ``LlamaRef.forward``  the dense causal forward over a whole token list (no cache): what
+                        prefill + decode must reproduce position by position
+* greedy sampling       sample_tokens with temperature 0 -> argmax, sampling.py:131-134
+
+Arithmetic is float32 (the north-star reference precision); the paged cache stores
+``cache_dtype`` (float16 by default, as KVCache(dtype=float16), kv_cache.py:25-32).
+Weights use the reference's Meta-style names (``layers.{i}.attention.wq.weight``, ...,
+llama.py:413-416).
+"""
+
+import numpy as np
+
+from .attention import flash_prefill_ref, paged_decode_ref
+
+
+def rms_norm_ref(x, weight, eps=1e-5):
+    """llama.py:21-23."""
+    x = np.asarray(x, dtype=np.float32)
+    rms = np.float32(1.0) / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + np.float32(eps))
+    return (x * rms * np.asarray(weight, dtype=np.float32)).astype(np.float32)
+
+
+def rope_tables_ref(head_dim, seq_len, theta=10000.0):
+    """llama.py:26-31: (cos, sin) of t * theta^(-arange(0, D, 2) / D), each [seq_len, D/2]."""
+    expo = np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim)
+    freqs = np.float32(1.0) / (np.float32(theta) ** expo)
+    t = np.arange(seq_len, dtype=np.float32)
+    ang = (t[:, None] * freqs[None, :]).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def apply_rope_ref(x, cos, sin):
+    """llama.py:34-55 on x [..., H, D] with cos/sin broadcastable to [..., 1, D/2]."""
+    x = np.asarray(x, dtype=np.float32)
+    x0, x1 = x[..., 0::2], x[..., 1::2]
+    out0 = x0 * cos - x1 * sin
+    out1 = x0 * sin + x1 * cos
+    return np.stack([out0, out1], axis=-1).reshape(x.shape).astype(np.float32)
+
+
+def silu_ref(x):
+    return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+def greedy_ref(logits):
+    """sampling.py:133-134: argmax over the vocabulary (first maximum)."""
+    return np.argmax(np.asarray(logits), axis=-1)
+
+
+class LlamaRef:
+    """The reference model's forward passes over numpy float32 weights."""
+
+    def __init__(self, cfg, weights, cache_dtype=np.float16):
+        self.cfg = cfg
+        self.w = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
+        self.cache_dtype = cache_dtype
+        self.head_dim = cfg.dim // cfg.n_heads
+        self.cos, self.sin = rope_tables_ref(self.head_dim, cfg.max_seq_len * 2, cfg.rope_theta)
+
+    def _lin(self, x, name):
+        return (x @ self.w[name].T).astype(np.float32)
+
+    def _qkv(self, i, x, pos):
+        """Projections + RoPE of tokens x [T, dim] at positions pos [T] (llama.py:178-182, 315-322)."""
+        c, d = self.cfg, self.head_dim
+        p = f"layers.{i}."
+        xn = rms_norm_ref(x, self.w[p + "attention_norm.weight"], c.norm_eps)
+        q = self._lin(xn, p + "attention.wq.weight").reshape(-1, c.n_heads, d)
+        k = self._lin(xn, p + "attention.wk.weight").reshape(-1, c.n_kv_heads, d)
+        v = self._lin(xn, p + "attention.wv.weight").reshape(-1, c.n_kv_heads, d)
+        cos, sin = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
+        return apply_rope_ref(q, cos, sin), apply_rope_ref(k, cos, sin), v
+
+    def _finish_layer(self, i, x, attn):
+        """wo, residual, FFN, residual (llama.py:186, 241-244, 334-338)."""
+        c = self.cfg
+        p = f"layers.{i}."
+        h = x + self._lin(attn.reshape(attn.shape[0], -1), p + "attention.wo.weight")
+        hn = rms_norm_ref(h, self.w[p + "ffn_norm.weight"], c.norm_eps)
+        ff = self._lin(silu_ref(self._lin(hn, p + "feed_forward.w1.weight")) * self._lin(hn, p + "feed_forward.w3.weight"),
+                       p + "feed_forward.w2.weight")
+        return (h + ff).astype(np.float32)
+
+    def _logits(self, x):
+        return self._lin(rms_norm_ref(x, self.w["norm.weight"], self.cfg.norm_eps), "output.weight")
+
+    def _store(self, cache, slot, value, block_size):
+        cache.reshape(-1, *cache.shape[2:])[slot] = value.astype(self.cache_dtype).astype(cache.dtype)
+
+    def forward(self, tokens):
+        """Dense causal forward over tokens [L] from position 0: logits [L, vocab]."""
+        tokens = np.asarray(tokens).reshape(-1)
+        x = self.w["tok_embeddings.weight"][tokens]
+        pos = np.arange(len(tokens))
+        for i in range(self.cfg.n_layers):
+            q, k, v = self._qkv(i, x, pos)
+            attn = flash_prefill_ref(q[None], k[None], v[None], True, acc=np.float32)[0]
+            x = self._finish_layer(i, x, attn)
+        return self._logits(x)
+
+    def prefill(self, tokens, k_caches, v_caches, block_table, start_pos, block_size):
+        """llama.py:264-285 for one sequence; writes the caches in place; logits [L, vocab]."""
+        tokens = np.asarray(tokens).reshape(-1)
+        x = self.w["tok_embeddings.weight"][tokens]
+        pos = start_pos + np.arange(len(tokens))
+        slots = np.asarray(block_table)[pos // block_size] * block_size + pos % block_size
+        for i in range(self.cfg.n_layers):
+            q, k, v = self._qkv(i, x, pos)
+            self._store(k_caches[i], slots, k, block_size)
+            self._store(v_caches[i], slots, v, block_size)
+            attn = flash_prefill_ref(q[None], k[None], v[None], True, acc=np.float32)[0]
+            x = self._finish_layer(i, x, attn)
+        return self._logits(x)
+
+    def decode(self, tokens, positions, context_lens, block_tables, k_caches, v_caches, block_size,
+               write_before_attend=True):
+        """One batched decode step (llama.py:290-388); writes the caches; logits [B, vocab]."""
+        c, d = self.cfg, self.head_dim
+        tokens = np.asarray(tokens).reshape(-1)
+        positions = np.asarray(positions).reshape(-1)
+        block_tables = np.asarray(block_tables)
+        x = self.w["tok_embeddings.weight"][tokens]
+        slots = block_tables[np.arange(len(tokens)), positions // block_size] * block_size + positions % block_size
+        for i in range(c.n_layers):
+            q, k, v = self._qkv(i, x, positions)
+            if write_before_attend:
+                self._store(k_caches[i], slots, k, block_size)
+                self._store(v_caches[i], slots, v, block_size)
+            attn = paged_decode_ref(q[:, None], k_caches[i], v_caches[i], block_tables, context_lens,
+                                    c.n_heads, c.n_kv_heads, d, block_size, acc=np.float32)[:, 0]
+            if not write_before_attend:
+                self._store(k_caches[i], slots, k, block_size)
+                self._store(v_caches[i], slots, v, block_size)
+            x = self._finish_layer(i, x, attn.astype(np.float32))
+        return self._logits(x)
+
+
+def reference_weight_names(n_layers):
+    """The per-model weight names of the reference's Meta-style map (llama.py:398-435)."""
+    names = ["tok_embeddings.weight", "norm.weight", "output.weight"]
+    for i in range(n_layers):
+        p = f"layers.{i}."
+        names += [p + s for s in ("attention.wq.weight", "attention.wk.weight", "attention.wv.weight",
+                                  "attention.wo.weight", "feed_forward.w1.weight", "feed_forward.w2.weight",
+                                  "feed_forward.w3.weight", "attention_norm.weight", "ffn_norm.weight")]
+    return names
+

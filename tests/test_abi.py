@@ -1,4 +1,4 @@
-"""The C ABI: libtvattn.so loads on the host and exports exactly what include/tv_attn.h declares.
+"""The C ABI: libtvattn.so loads on the host and exports exactly what include/*.h declares.
 
 Only host-side entry points run here (no kernel launch): argument validation
 paths return before any HIP call.
@@ -12,32 +12,35 @@ import pytest
 
 from tinyvllm_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "tv_attn.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+
+
+def header_text():
+    return re.sub(r"/\*.*?\*/", "", "\n".join(h.read_text() for h in HEADERS), flags=re.S)
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(tv_[a-z_0-9]+)\s*\(", text, flags=re.M))
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(tv_[a-z_0-9]+)\s*\(", header_text(), flags=re.M))
 
 
 def test_header_parses():
     names = declared_functions()
     assert {"tv_paged_decode", "tv_flash_prefill", "tv_reshape_and_cache", "tv_write_kv",
             "tv_read_kv_blocks", "tv_last_error", "tv_abi_version",
-            "tv_paged_decode_workspace_bytes"} <= names
+            "tv_paged_decode_workspace_bytes", "tv_linear", "tv_rms_norm_residual", "tv_qkv_rope_cache",
+            "tv_argmax_advance", "tv_llama_decode_step", "tv_llama_prefill", "tv_llama_graph_create"} <= names
 
 
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():
-        assert hasattr(lib, name), f"{name} declared in tv_attn.h but not exported"
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
     assert set(_lib.SIGNATURES) == declared_functions()
     assert lib.tv_abi_version() == _lib.ABI_VERSION
 
 
 def test_argument_counts_match_header():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = header_text()
     for name, (_, args) in _lib.SIGNATURES.items():
         m = re.search(name + r"\s*\(([^)]*)\)", text)
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
@@ -105,3 +108,42 @@ def test_no_bit_cast_of_vector_element_lvalues():
             if re.search(r"__builtin_bit_cast\(\s*\w+\s*,\s*\w+(\[[^\]]*\])+\s*\)", line):
                 bad.append(f"{f.name}:{n}: {line.strip()}")
     assert not bad, "\n".join(bad)
+
+
+def test_linear_split_choice():
+    """K splits the decode step uses: about one work-group per CU, whole 256-wide
+    K chunks, and one split once the output tiles alone fill the GPU."""
+    lib = _lib.load()
+    assert lib.tv_linear_k_split(64, 2560, 2048) == 256        # q|k|v: 40 tiles x 8 splits
+    assert lib.tv_linear_k_split(64, 2048, 5632) == 768        # down projection
+    assert lib.tv_linear_k_split(64, 11264, 2048) == 2048      # w1|w3: 176 tiles, one split
+    assert lib.tv_linear_k_split(1024, 2560, 2048) == 2048     # prefill rows fill the GPU
+    assert lib.tv_linear_k_split(4, 96, 64) % 32 == 0
+
+
+def test_dense_entry_points_validate_on_host():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    # K not a multiple of 32, N not a multiple of 4, bad dtype, multi-split logits
+    assert lib.tv_linear(p, p, p, 4, 64, 48, 48, 0, 48, 0, None, _lib.TV_F16, None) == _lib.TV_EUNSUPPORTED
+    assert lib.tv_linear(p, p, p, 4, 66, 64, 64, 0, 64, 0, None, _lib.TV_F16, None) == _lib.TV_EUNSUPPORTED
+    assert lib.tv_linear(p, p, p, 4, 64, 64, 64, 0, 64, 0, None, _lib.TV_F32, None) == _lib.TV_EUNSUPPORTED
+    assert lib.tv_linear(p, p, p, 4, 64, 64, 64, 64, 32, 2, None, _lib.TV_F16, None) == _lib.TV_EINVAL
+    assert b"one split" in lib.tv_last_error()
+    assert lib.tv_qkv_rope_cache(p, None, None, p, None, p, 1, None, 0, p, 8, p, 0, 1, 16, 4, 1, 4, 2, 16,
+                                 _lib.TV_F16, None, None, None) == _lib.TV_EINVAL
+    assert lib.tv_llama_decode_step(None, None, None, None) == _lib.TV_EINVAL
+    assert lib.tv_llama_graph_create(None, None, None, None, None) == _lib.TV_EINVAL
+
+
+def test_decode_step_workspace_tinyllama():
+    """Workspace of the TinyLlama-1.1B step at batch 64 (the config-4 shape)."""
+    from tinyvllm_amd.llama import LlamaConfig, _Model
+    c = LlamaConfig.tinyllama_1b()
+    m = _Model(c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim, c.hidden_dim, c.vocab_size, _lib.TV_F16,
+               c.norm_eps)
+    lib = _lib.load()
+    ws = lib.tv_llama_decode_workspace_bytes(ctypes.byref(m), 64, 72, 16, 2048)
+    # 8 split partials of the widest product + activations + 500 x 64 argmax keys
+    assert 64 * 2560 * 8 * 4 < ws < 16 << 20
+    assert lib.tv_llama_decode_workspace_bytes(ctypes.byref(m), 0, 72, 16, 2048) == 0

@@ -1,0 +1,445 @@
+"""Decode-step kernels and the LLaMA model on the GPU vs the oracle (oracle/llama.py).
+
+Kernel level (through the C ABI, include/tv_llama.h): the skinny MFMA product
+with its three epilogues against numpy, RMSNorm + residual, RoPE + K/V cache
+write (slot placement bit-exact), greedy sampling / advance.
+Model level: prefill and batched decode of small configs and of the TinyLlama
+1.1B shape against the float32 oracle (logits <= 2e-2 max-abs, the fp16 bar),
+the reference's K/V order, graph replay vs eager launches (bit-identical, the
+reference's determinism test, test_jit_decode.py:138-171), and the
+device-resident multi-step loop.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.llama import LlamaRef, apply_rope_ref, greedy_ref, rms_norm_ref, rope_tables_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def lib():
+    from tinyvllm_amd import _lib
+    return _lib.load()
+
+
+def check(rc, what):
+    from tinyvllm_amd import _lib
+    _lib.check(rc, what)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def gen(seed, *shape, dtype=torch.float16, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return torch.from_numpy((scale * rng.standard_normal(shape)).astype(np.float32)).to(dtype).cuda()
+
+
+def f64(t):
+    return t.double().cpu().numpy()
+
+
+# ---- linear -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,ks", [(1, 64, 32, 32), (5, 100, 96, 32), (64, 2560, 2048, 256),
+                                      (70, 132, 320, 64), (130, 64, 512, 512), (64, 2048, 5632, 768),
+                                      (3, 40, 800, 800)])
+def test_linear_partial(dtype, M, N, K, ks):
+    from tinyvllm_amd._lib import dtype_code
+    a = gen(1, M, K, dtype=dtype)
+    w = gen(2, N, K, dtype=dtype, scale=0.05)
+    splits = -(-K // ks)
+    part = torch.full((splits, M, N), float("nan"), dtype=torch.float32, device="cuda")
+    check(lib().tv_linear(ptr(part), ptr(a), ptr(w), M, N, K, K, 0, ks, 0, None, dtype_code(dtype), None), "linear")
+    torch.cuda.synchronize()
+    A, W, P = f64(a), f64(w), part.double().cpu().numpy()
+    for s in range(splits):
+        want = A[:, s * ks:(s + 1) * ks] @ W[:, s * ks:(s + 1) * ks].T
+        assert np.abs(P[s] - want).max() < 1e-4 * max(1.0, np.abs(want).max()), s
+
+
+def test_linear_strided_a():
+    """A rows at a stride larger than K (a view into a wider activation buffer)."""
+    from tinyvllm_amd._lib import TV_F16
+    big = gen(3, 9, 160)
+    a = big[:, :96]
+    w = gen(4, 64, 96, scale=0.05)
+    part = torch.empty((1, 9, 64), dtype=torch.float32, device="cuda")
+    check(lib().tv_linear(ptr(part), ptr(a), ptr(w), 9, 64, 96, 160, 0, 96, 0, None, TV_F16, None), "linear")
+    torch.cuda.synchronize()
+    assert np.abs(part[0].double().cpu().numpy() - f64(a) @ f64(w).T).max() < 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,H,K", [(4, 48, 64), (64, 5632, 2048), (65, 96, 256)])
+def test_linear_swiglu(dtype, M, H, K):
+    from tinyvllm_amd._lib import dtype_code
+    a = gen(5, M, K, dtype=dtype)
+    w1 = gen(6, H, K, dtype=dtype, scale=0.04)
+    w3 = gen(7, H, K, dtype=dtype, scale=0.04)
+    w13 = torch.stack([w1.view(H // 2, 2, K), w3.view(H // 2, 2, K)], 1).reshape(2 * H, K).contiguous()
+    out = torch.full((M, H), float("nan"), dtype=dtype, device="cuda")
+    check(lib().tv_linear(ptr(out), ptr(a), ptr(w13), M, 2 * H, K, K, H, K, 1, None, dtype_code(dtype), None),
+          "swiglu")
+    torch.cuda.synchronize()
+    g, u = f64(a) @ f64(w1).T, f64(a) @ f64(w3).T
+    want = g / (1 + np.exp(-g)) * u
+    assert np.abs(out.double().cpu().numpy() - want).max() < TOL * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 100, 64), (64, 32000, 2048), (70, 260, 96)])
+def test_linear_logits_and_greedy(M, N, K):
+    from tinyvllm_amd._lib import TV_F16
+    a = gen(8, M, K)
+    w = gen(9, N, K, scale=0.05)
+    logits = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    nparts = -(-N // 64)
+    keys = torch.zeros((nparts, M), dtype=torch.int64, device="cuda")
+    check(lib().tv_linear(ptr(logits), ptr(a), ptr(w), M, N, K, K, N, K, 2, ptr(keys), TV_F16, None), "logits")
+    toks = torch.zeros(M, dtype=torch.int32, device="cuda")
+    check(lib().tv_argmax_advance(ptr(toks), None, None, None, 0, ptr(keys), nparts, M, None), "argmax")
+    torch.cuda.synchronize()
+    L = logits.double().cpu().numpy()
+    want = f64(a) @ f64(w).T
+    assert np.abs(L - want).max() < 1e-4 * max(1.0, np.abs(want).max())
+    # the sampled token is the first maximum of the very values written
+    assert np.array_equal(toks.cpu().numpy(), np.argmax(logits.cpu().numpy(), axis=1))
+
+
+def test_greedy_tie_resolves_to_first_index():
+    """Two identical, dominant rows in different work-group tiles (5 and 70): every
+    token ties between them and must take 5 (numpy / tinygrad argmax semantics)."""
+    from tinyvllm_amd._lib import TV_F16
+    M, N, K = 7, 128, 64
+    a = gen(30, M, K).abs()
+    w = gen(31, N, K, scale=0.01)
+    w[5] = 0.5
+    w[70] = 0.5
+    keys = torch.zeros((2, M), dtype=torch.int64, device="cuda")
+    check(lib().tv_linear(None, ptr(a), ptr(w), M, N, K, K, N, K, 2, ptr(keys), TV_F16, None), "logits")
+    toks = torch.zeros(M, dtype=torch.int32, device="cuda")
+    check(lib().tv_argmax_advance(ptr(toks), None, None, None, 0, ptr(keys), 2, M, None), "argmax")
+    torch.cuda.synchronize()
+    assert toks.cpu().tolist() == [5] * M
+
+
+def test_argmax_advance_updates_state():
+    from tinyvllm_amd._lib import TV_F16
+    M, N, K = 4, 128, 32
+    a, w = gen(10, M, K), gen(11, N, K)
+    keys = torch.zeros((2, M), dtype=torch.int64, device="cuda")
+    check(lib().tv_linear(None, ptr(a), ptr(w), M, N, K, K, N, K, 2, ptr(keys), TV_F16, None), "logits")
+    toks = torch.zeros(M, dtype=torch.int32, device="cuda")
+    pos = torch.tensor([0, 5, 9, 3], dtype=torch.int32, device="cuda")
+    ctx = pos + 1
+    hist = torch.full((M, 8), -1, dtype=torch.int32, device="cuda")
+    check(lib().tv_argmax_advance(ptr(toks), ptr(pos), ptr(ctx), ptr(hist), 8, ptr(keys), 2, M, None), "adv")
+    torch.cuda.synchronize()
+    want = np.argmax(f64(a) @ f64(w).T, axis=1)
+    assert np.array_equal(toks.cpu().numpy(), want)
+    assert pos.tolist() == [1, 6, 10, 4] and ctx.tolist() == [2, 7, 11, 5]
+    h = hist.cpu().numpy()
+    assert h[0, 1] == want[0] and h[1, 6] == want[1] and h[3, 4] == want[3]
+    assert (h[2] == -1).all()                  # position 9 + 1 is past the history width: not written
+    assert (h == -1).sum() == 4 * 8 - 3
+
+
+# ---- norm / rope --------------------------------------------------------------------------
+
+def test_rms_norm_residual_embed_and_add():
+    from tinyvllm_amd._lib import TV_F16
+    M, dim, V = 6, 256, 50
+    emb = gen(12, V, dim)
+    w = gen(13, dim, dtype=torch.float32, scale=0.3) + 1
+    toks = torch.tensor([0, 7, 49, 3, 3, 22], dtype=torch.int32, device="cuda")
+    x = torch.empty((M, dim), dtype=torch.float32, device="cuda")
+    xh = torch.empty((M, dim), dtype=torch.float16, device="cuda")
+    check(lib().tv_rms_norm_residual(ptr(x), ptr(xh), None, 0, ptr(emb), ptr(toks), V, ptr(w), M, dim, 1e-5,
+                                     TV_F16, None), "embed")
+    torch.cuda.synchronize()
+    X = emb.float().cpu().numpy()[toks.cpu().numpy()]
+    assert np.array_equal(x.cpu().numpy(), X)
+    want = rms_norm_ref(X, w.cpu().numpy())
+    assert np.abs(xh.float().cpu().numpy() - want).max() < 2e-3 * np.abs(want).max()
+    part = gen(14, 3, M, dim, dtype=torch.float32)
+    check(lib().tv_rms_norm_residual(ptr(x), ptr(xh), ptr(part), 3, None, None, 0, ptr(w), M, dim, 1e-5,
+                                     TV_F16, None), "residual")
+    torch.cuda.synchronize()
+    P = part.cpu().numpy()
+    X2 = ((X + P[0]) + P[1]) + P[2]
+    assert np.abs(x.cpu().numpy() - X2).max() < 1e-6
+    want = rms_norm_ref(X2, w.cpu().numpy())
+    assert np.abs(xh.float().cpu().numpy() - want).max() < 2e-3 * np.abs(want).max()
+
+
+def test_rope_table_matches_oracle():
+    """Table vs the float64 closed form.  The reference computes the angles in
+    float32 (llama.py:28-30), so an ulp of a frequency grows with the position:
+    the bound is 4 ulps of the float32 angle (plus cos/sin rounding); the oracle's
+    own float32 table obeys the same bound."""
+    P, D = 512, 64
+    t = torch.empty((P, D // 2, 2), dtype=torch.float32, device="cuda")
+    check(lib().tv_rope_table(ptr(t), P, D, 10000.0, None), "rope_table")
+    torch.cuda.synchronize()
+    ang = np.arange(P)[:, None] * (10000.0 ** (-np.arange(0, D, 2) / D))[None]
+    bound = 4 * np.spacing(ang.astype(np.float32)).astype(np.float64) + 2e-7
+    T = t.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(T[..., 0] - np.cos(ang)) <= bound) and np.all(np.abs(T[..., 1] - np.sin(ang)) <= bound)
+    cos, sin = rope_tables_ref(D, P)
+    assert np.all(np.abs(cos - np.cos(ang)) <= bound) and np.all(np.abs(sin - np.sin(ang)) <= bound)
+
+
+@pytest.mark.parametrize("write_cache", [True, False])
+def test_qkv_rope_cache(write_cache):
+    from tinyvllm_amd._lib import TV_F16
+    M, Hq, Hkv, D, bs, NB, splits = 5, 4, 2, 32, 4, 12, 3
+    N = (Hq + 2 * Hkv) * D
+    part = gen(15, splits, M, N, dtype=torch.float32)
+    rope = torch.empty((64, D // 2, 2), dtype=torch.float32, device="cuda")
+    check(lib().tv_rope_table(ptr(rope), 64, D, 10000.0, None), "rope")
+    pos = torch.tensor([0, 3, 9, 14, 40], dtype=torch.int32, device="cuda")
+    bt_np = np.array([[5, 1, 0, 0], [2, 0, 0, 0], [7, 9, 11, 0], [3, 4, 6, 8], [10, 0, 0, 0]], dtype=np.int32)
+    bt_np[1, 0] = 99                          # row 1's block is outside the cache: not written, counted
+    bt = torch.from_numpy(bt_np).cuda()        # row 4's position 40 is past its table (4 blocks of 4): counted
+    q = torch.empty((M, Hq * D), dtype=torch.float16, device="cuda")
+    ko = torch.empty((M, Hkv * D), dtype=torch.float16, device="cuda")
+    vo = torch.empty_like(ko)
+    kc = torch.zeros((NB, bs, Hkv, D), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    slots = torch.full((M,), 123, dtype=torch.int32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    check(lib().tv_qkv_rope_cache(ptr(q), ptr(ko), ptr(vo), ptr(kc) if write_cache else None,
+                                  ptr(vc) if write_cache else None, ptr(part), splits, ptr(pos), 0, ptr(rope), 64,
+                                  ptr(bt), 4, 4, bs, NB, M, Hq, Hkv, D, TV_F16, ptr(slots), ptr(err), None), "qkv")
+    torch.cuda.synchronize()
+    S = part.cpu().numpy().sum(0)
+    P = pos.cpu().numpy()
+    cos, sin = rope_tables_ref(D, 64)
+    c, s = cos[P][:, None], sin[P][:, None]
+    wq = apply_rope_ref(S[:, :Hq * D].reshape(M, Hq, D), c, s)
+    wk = apply_rope_ref(S[:, Hq * D:(Hq + Hkv) * D].reshape(M, Hkv, D), c, s)
+    wv = S[:, (Hq + Hkv) * D:].reshape(M, Hkv, D)
+    assert np.abs(q.float().cpu().numpy().reshape(M, Hq, D) - wq).max() < 4e-3 * np.abs(wq).max()
+    assert np.abs(ko.float().cpu().numpy().reshape(M, Hkv, D) - wk).max() < 4e-3 * np.abs(wk).max()
+    assert np.abs(vo.float().cpu().numpy().reshape(M, Hkv, D) - wv).max() < 4e-3 * np.abs(wv).max()
+    want_slots = [5 * 4 + 0, -1, 11 * 4 + 1, 8 * 4 + 2, -1]
+    assert slots.cpu().tolist() == want_slots and err.item() == 2
+    K, Vc = kc.cpu().numpy().reshape(NB * bs, Hkv, D), vc.cpu().numpy().reshape(NB * bs, Hkv, D)
+    if write_cache:
+        written = {sl: m for m, sl in enumerate(want_slots) if sl >= 0}
+        for sl in range(NB * bs):
+            if sl in written:
+                m = written[sl]
+                assert np.array_equal(K[sl], ko.cpu().numpy().reshape(M, Hkv, D)[m])
+                assert np.array_equal(Vc[sl], vo.cpu().numpy().reshape(M, Hkv, D)[m])
+            else:
+                assert not K[sl].any() and not Vc[sl].any()
+    else:
+        assert not K.any() and not Vc.any()
+
+
+# ---- model ------------------------------------------------------------------------------------
+
+def small_config(**kw):
+    from tinyvllm_amd.llama import LlamaConfig
+    args = dict(dim=128, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=512, hidden_dim=256, max_seq_len=128,
+                dtype="float16")
+    args.update(kw)
+    return LlamaConfig(**args)
+
+
+def numpy_weights(weights):
+    return {k: v.float().cpu().numpy() for k, v in weights.items()}
+
+
+def build(cfg, seed=0, std=0.05, write_before_attend=True, num_blocks=64, block_size=16):
+    from tinyvllm_amd.block_manager import BlockManager
+    from tinyvllm_amd.kv_cache import KVCache
+    from tinyvllm_amd.llama import Llama, random_weights
+    weights = random_weights(cfg, seed=seed, std=std)
+    # non-trivial norm weights so the norm weight path is exercised
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    for k in list(weights):
+        if k.endswith("norm.weight"):
+            weights[k] = 1 + 0.2 * torch.randn(weights[k].shape, generator=g, device="cuda")
+    model = Llama(cfg, weights, write_before_attend=write_before_attend)
+    kv = KVCache(cfg.n_layers, num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
+    bm = BlockManager(1, num_blocks, block_size)
+    ref = LlamaRef(cfg, numpy_weights(weights), cache_dtype=np.float16)
+    shape = (num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim)
+    rk = [np.zeros(shape, np.float32) for _ in range(cfg.n_layers)]
+    rv = [np.zeros(shape, np.float32) for _ in range(cfg.n_layers)]
+    return model, kv, bm, ref, rk, rv
+
+
+def max_err(got, want):
+    return float(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64)).max())
+
+
+def test_prefill_matches_oracle():
+    cfg = small_config()
+    model, kv, bm, ref, rk, rv = build(cfg)
+    rng = np.random.default_rng(20)
+    for sid, n in enumerate([5, 17, 33]):
+        bm.register_sequence(sid)
+        toks = rng.integers(0, cfg.vocab_size, n)
+        logits = model.prefill(toks, kv, bm, sid)[0].cpu().numpy()
+        want = ref.prefill(toks, rk, rv, np.array(bm.get_block_table(sid)), 0, 16)
+        assert max_err(logits, want) < TOL, sid
+        assert bm.get_context_length(sid) == n
+    for layer in range(cfg.n_layers):
+        assert max_err(kv.k_cache[layer].float().cpu().numpy(), rk[layer]) < 4e-3
+        assert max_err(kv.v_cache[layer].float().cpu().numpy(), rv[layer]) < 4e-3
+
+
+def prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg):
+    """Prefill each sequence on both sides; returns the oracle's next tokens."""
+    nxt = []
+    for sid, n in enumerate(lens):
+        bm.register_sequence(sid)
+        toks = rng.integers(0, cfg.vocab_size, n)
+        model.prefill(toks, kv, bm, sid, logits=None)
+        want = ref.prefill(toks, rk, rv, np.array(bm.get_block_table(sid)), 0, kv.block_size)
+        nxt.append(int(greedy_ref(want[-1])))
+    return nxt
+
+
+@pytest.mark.parametrize("write_before_attend", [True, False])
+def test_decode_steps_match_oracle(write_before_attend):
+    """Engine convention (context = position + 1, engine.py:251) over several steps,
+    teacher-forced with the oracle's greedy tokens."""
+    cfg = small_config()
+    model, kv, bm, ref, rk, rv = build(cfg, seed=3, write_before_attend=write_before_attend)
+    rng = np.random.default_rng(21)
+    lens = [7, 16, 30, 1]
+    toks = prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg)
+    jit = model.create_jit_decode(16)
+    max_blocks = 4
+    for step in range(4):
+        pos = [bm.seq_positions[s] for s in range(len(lens))]
+        for s, p in enumerate(pos):
+            bm.ensure_block_for_position(s, p)
+        bt = np.zeros((len(lens), max_blocks), np.int32)
+        for s in range(len(lens)):
+            t = bm.get_block_table(s)
+            bt[s, :len(t)] = t
+        ctx = [p + 1 for p in pos]
+        logits = model.decode(torch.tensor(toks).reshape(-1, 1), kv, bm, list(range(len(lens))), pos,
+                              torch.from_numpy(bt), torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
+        want = ref.decode(toks, pos, ctx, bt, rk, rv, 16, write_before_attend=write_before_attend)
+        assert logits.shape == (len(lens), 1, cfg.vocab_size)
+        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        toks = [int(t) for t in greedy_ref(want)]
+    for layer in range(cfg.n_layers):
+        assert max_err(kv.k_cache[layer].float().cpu().numpy(), rk[layer]) < 4e-3
+
+
+def test_graph_replay_is_deterministic_and_equals_eager():
+    from tinyvllm_amd.llama import DecodeGraph
+    cfg = small_config(n_layers=3)
+    model, kv, bm, ref, rk, rv = build(cfg, seed=5)
+    rng = np.random.default_rng(22)
+    toks = prefill_batch(model, kv, bm, ref, rk, rv, [9, 12, 20], rng, cfg)
+    pos = [9, 12, 20]
+    bt = np.zeros((3, 4), np.int32)
+    for s in range(3):
+        bm.ensure_block_for_position(s, pos[s])
+        t = bm.get_block_table(s)
+        bt[s, :len(t)] = t
+    g = DecodeGraph(model, kv, 3, 4)
+    outs = []
+    for mode in ("eager", "graph", "graph"):
+        g.set_inputs(toks, pos, [p + 1 for p in pos], bt)
+        if mode == "eager":
+            g.step_eager()
+        else:
+            g.step()
+        torch.cuda.synchronize()
+        outs.append((g.logits.clone(), g.tokens.clone(), g.positions.clone(), g.context_lens.clone()))
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            assert torch.equal(a, b)
+    assert outs[0][2].tolist() == [p + 1 for p in pos] and outs[0][3].tolist() == [p + 2 for p in pos]
+    assert outs[0][1].tolist() == np.argmax(outs[0][0].cpu().numpy(), axis=1).tolist()
+
+
+def test_device_loop_matches_host_stepping():
+    """run(n) with sampling, position advance and history on the device equals n
+    steps fed from the host."""
+    from tinyvllm_amd.llama import DecodeGraph
+    cfg = small_config()
+    model, kv, bm, ref, rk, rv = build(cfg, seed=6, num_blocks=32)
+    rng = np.random.default_rng(23)
+    lens = [4, 11]
+    toks = prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg)
+    steps = 6
+    bt = np.zeros((2, 4), np.int32)
+    for s in range(2):
+        bm.ensure_block_for_position(s, lens[s] + steps)
+        t = bm.get_block_table(s)
+        bt[s, :len(t)] = t
+    snapshot = [(k.clone(), v.clone()) for k, v in zip(kv.k_cache, kv.v_cache)]
+    g = DecodeGraph(model, kv, 2, 4, history_len=32)
+    g.set_inputs(toks, lens, [n + 1 for n in lens], bt)
+    g.run(steps)
+    torch.cuda.synchronize()
+    hist = g.history.cpu().numpy()
+    dev_tokens = [hist[s, lens[s] + 1:lens[s] + 1 + steps].tolist() for s in range(2)]
+    for (k, v), (k0, v0) in zip(zip(kv.k_cache, kv.v_cache), snapshot):
+        k.copy_(k0)
+        v.copy_(v0)
+    h = DecodeGraph(model, kv, 2, 4)
+    cur = list(toks)
+    host_tokens = [[], []]
+    for i in range(steps):
+        h.set_inputs(cur, [n + i for n in lens], [n + i + 1 for n in lens], bt)
+        h.step()
+        cur = h.tokens.cpu().tolist()
+        for s in range(2):
+            host_tokens[s].append(cur[s])
+    assert dev_tokens == host_tokens
+    assert g.positions.cpu().tolist() == [n + steps for n in lens]
+
+
+def test_tinyllama_shape_matches_oracle():
+    """TinyLlama-1.1B architecture (22 layers, dim 2048, 32/4 heads, MLP 5632,
+    vocab 32000), random N(0, 0.02) fp16 weights: prefill + 2 decode steps."""
+    from tinyvllm_amd.llama import LlamaConfig
+    cfg = LlamaConfig.tinyllama_1b()
+    model, kv, bm, ref, rk, rv = build(cfg, seed=7, std=0.02, num_blocks=16)
+    rng = np.random.default_rng(24)
+    lens = [8, 13, 16]
+    nxt = []
+    for sid, n in enumerate(lens):
+        bm.register_sequence(sid)
+        toks = rng.integers(0, cfg.vocab_size, n)
+        logits = model.prefill(toks, kv, bm, sid, logits="last")[0, 0].cpu().numpy()
+        want = ref.prefill(toks, rk, rv, np.array(bm.get_block_table(sid)), 0, 16)[-1]
+        assert max_err(logits, want) < TOL, sid
+        nxt.append(int(greedy_ref(want)))
+    jit = model.create_jit_decode(16)
+    for step in range(2):
+        pos = [bm.seq_positions[s] for s in range(3)]
+        bt = np.zeros((3, 2), np.int32)
+        for s in range(3):
+            bm.ensure_block_for_position(s, pos[s])
+            t = bm.get_block_table(s)
+            bt[s, :len(t)] = t
+        ctx = [p + 1 for p in pos]
+        logits = model.decode(torch.tensor(nxt).reshape(-1, 1), kv, bm, [0, 1, 2], pos, torch.from_numpy(bt),
+                              torch.tensor(ctx, dtype=torch.int32), jit, 2)
+        want = ref.decode(nxt, pos, ctx, bt, rk, rv, 16)
+        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        top2 = np.sort(want, axis=1)[:, -2:]
+        clear = top2[:, 1] - top2[:, 0] > 2 * TOL
+        got_tok = logits[:, 0].cpu().numpy().argmax(1)
+        assert np.array_equal(got_tok[clear], greedy_ref(want)[clear])
+        nxt = [int(t) for t in greedy_ref(want)]

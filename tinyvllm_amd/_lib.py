@@ -1,4 +1,4 @@
-"""ctypes binding of libtvattn.so (declarations: include/tv_attn.h).
+"""ctypes binding of libtvattn.so (declarations: include/tv_attn.h, include/tv_llama.h).
 
 The library is required: importing the ops without it raises immediately, and
 there is no CPU or PyTorch fallback for any op.
@@ -31,8 +31,23 @@ SIGNATURES = {
     "tv_reshape_and_cache": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _L, _L, _I, _P, _P]),
     "tv_write_kv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _L, _L, _I, _P]),
     "tv_read_kv_blocks": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    # include/tv_llama.h
+    "tv_linear_k_split": (_I, [_I, _I, _I]),
+    "tv_linear": (_I, [_P, _P, _P, _I, _I, _I, _L, _L, _I, _I, _P, _I, _P]),
+    "tv_rms_norm_residual": (_I, [_P, _P, _P, _I, _P, _P, _I, _P, _I, _I, _F, _I, _P]),
+    "tv_rope_table": (_I, [_P, _I, _I, _F, _P]),
+    "tv_qkv_rope_cache": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _P, _L, _I, _I, _I, _I, _I, _I, _I,
+                               _I, _P, _P, _P]),
+    "tv_argmax_advance": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _P]),
+    "tv_llama_decode_workspace_bytes": (_S, [_P, _I, _I, _I, _I]),
+    "tv_llama_decode_step": (_I, [_P, _P, _P, _P]),
+    "tv_llama_graph_create": (_I, [_P, _P, _P, _P, _P]),
+    "tv_llama_graph_launch": (_I, [_P, _P]),
+    "tv_llama_graph_destroy": (_I, [_P]),
+    "tv_llama_prefill_workspace_bytes": (_S, [_P, _I]),
+    "tv_llama_prefill": (_I, [_P, _P, _P, _P]),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 

@@ -1,0 +1,370 @@
+// Dense kernels of the batched decode step (gfx950): the weight-streaming
+// products, RMSNorm with the residual add, RoPE with the K/V cache write, and
+// greedy sampling.  Semantics follow tinyvllm/model/llama.py:
+//   RMSNorm          x * rsqrt(mean(x^2) + eps) * w              llama.py:14-23
+//   RoPE table       cos/sin(p * theta^(-2i/D))                  llama.py:26-31
+//   RoPE             interleaved pairs (2i, 2i+1)                llama.py:34-55
+//   SwiGLU           w2(silu(w1 x) * w3 x)                       llama.py:220-221
+//   greedy sampling  argmax over the vocabulary (first maximum)  sampling.py:131-134
+//
+// linear_kernel computes Y = A W^T for a skinny A (the decode batch, M <= 64
+// per work-group) against a weight matrix W [N, K] that is streamed from HBM
+// exactly once.  Each of the 4 waves of a work-group owns 16 rows of W and all
+// 64 rows of A; A is staged in LDS per 256-wide K chunk and shared by the
+// waves.  W rows are the MFMA A operand (lane = output feature), A^T the B
+// operand (lane = token), so a lane ends up holding 4 consecutive output
+// features of one token: the layout the fused epilogues want.
+#include "tv_common.h"
+#include "tv_dense.h"
+
+namespace tv {
+
+// ---------------------------------------------------------------------------
+// Y = A W^T
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
+  // order-preserving map of the float to an unsigned key; ties resolve to the
+  // smallest index, as numpy / tinygrad argmax return the first maximum
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (0xFFFFFFFFu - (uint32_t)n);
+}
+
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit dwords, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned long long bytes) {
+  const unsigned n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (unsigned)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+template <typename T, int EPI>
+__global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
+  constexpr int KP = kLinKC + 8;   // LDS pitch (elements): 16-byte reads of 16 rows hit distinct banks
+  __shared__ __attribute__((aligned(16))) uint16_t sa[kLinBM * KP];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: W resource in SGPRs
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int n_wave = blockIdx.x * kLinBN + wave * 16;
+  const int m0 = blockIdx.z * kLinBM;
+  const int kb = blockIdx.y * p.k_split;
+  const int ke = min(kb + p.k_split, p.K);
+  const int nc = (ke - kb + kLinKC - 1) / kLinKC;
+
+  // Buffer loads: reads past the end of W (rows >= N) or of A (rows >= M)
+  // return zero in hardware, so no address is clamped and every offset inside
+  // a chunk is an immediate.
+  const long long w_rows = max(p.N - n_wave, 0);
+  const __amdgpu_buffer_rsrc_t wres = make_rsrc(reinterpret_cast<const T*>(p.w) + (size_t)min(n_wave, p.N) * p.K,
+                                                (unsigned long long)w_rows * p.K * sizeof(T));
+  const __amdgpu_buffer_rsrc_t ares = make_rsrc(reinterpret_cast<const T*>(p.a) + (size_t)m0 * p.lda,
+                                                (unsigned long long)max(p.M - m0, 0) * p.lda * sizeof(T));
+  const int w_voff = (col * p.K + kb + 8 * g) * (int)sizeof(T);
+  const int a_voff = ((tid >> 5) * (int)p.lda + kb + 8 * (tid & 31)) * (int)sizeof(T);
+  const int a_rows8 = 8 * (int)p.lda * (int)sizeof(T);   // byte step between the 8 rows a thread loads
+
+  // W: lane (row col, k group g) reads 8 elements per 32-wide k step.  Columns
+  // past the split are multiplied by zero rows of A.
+  auto loadW = [&](int c, u32x4 (&r)[8]) {
+    const int off = w_voff + c * kLinKC * (int)sizeof(T);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) r[s] = buffer_load16(wres, off + 64 * s, 0);
+  };
+  // A chunk: 64 rows x 32 vectors of 8 elements; thread tid loads vector
+  // tid % 32 of rows tid / 32 + 8 i.  Columns past the split are zeroed when
+  // stored to LDS (not at load time, so the loads stay in flight while the
+  // previous chunk computes).
+  auto loadA = [&](int c, u32x4 (&r)[8], bool& valid) {
+    valid = kb + c * kLinKC + 8 * (tid & 31) < ke;
+    const int off = a_voff + c * kLinKC * (int)sizeof(T);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = buffer_load16(ares, off, i * a_rows8);
+  };
+  auto storeA = [&](const u32x4 (&r)[8], bool valid) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<u32x4*>(&sa[((tid >> 5) + 8 * i) * KP + 8 * (tid & 31)]) = valid ? r[i] : u32x4{0, 0, 0, 0};
+  };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // All 8 k steps run even on a partial chunk: the A rows there are zero.
+  // The B fragments of step s + 1 are read from LDS while step s multiplies.
+  auto compute = [&](const u32x4 (&r)[8]) {
+    u32x4 b[2][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) b[0][mb] = *reinterpret_cast<const u32x4*>(&sa[(mb * 16 + col) * KP + 8 * g]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s + 1 < 8) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+          b[(s + 1) & 1][mb] = *reinterpret_cast<const u32x4*>(&sa[(mb * 16 + col) * KP + 32 * (s + 1) + 8 * g]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma16x16x32<T>(r[s], b[s & 1][mb], acc[mb]);
+    }
+  };
+
+  u32x4 w0[8], w1[8], ar[8];
+  bool av;
+  loadW(0, w0);
+  loadA(0, ar, av);
+  if (nc == 1) {
+    storeA(ar, av);
+    lds_barrier();
+    compute(w0);
+  } else {
+    // W and A of chunk c + 1 are in flight while chunk c computes.  The loads
+    // are unconditional (the last chunk is re-read) so the compiler can wait
+    // for exactly the chunk it needs.
+    for (int c = 0; c < nc; c += 2) {
+      loadW(min(c + 1, nc - 1), w1);
+      lds_barrier();
+      storeA(ar, av);
+      lds_barrier();
+      loadA(min(c + 1, nc - 1), ar, av);
+      compute(w0);
+      if (c + 1 >= nc) break;
+      loadW(min(c + 2, nc - 1), w0);
+      lds_barrier();
+      storeA(ar, av);
+      lds_barrier();
+      loadA(min(c + 2, nc - 1), ar, av);
+      compute(w1);
+    }
+  }
+
+  // lane holds acc[mb][i] = Y[m0 + 16 mb + col][n_wave + 4 g + i]
+  const int n = n_wave + 4 * g;
+  if constexpr (EPI == kEpiPartial) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = m0 + mb * 16 + col;
+      if (m < p.M && n < p.N)
+        *reinterpret_cast<f32x4*>(p.part + ((size_t)blockIdx.y * p.M + m) * p.N + n) = acc[mb];
+    }
+  } else if constexpr (EPI == kEpiSwiglu) {
+    // rows 4j, 4j+1 of W are w1 rows 2j, 2j+1; rows 4j+2, 4j+3 the matching w3 rows
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = m0 + mb * 16 + col;
+      if (m < p.M && n < p.N) {
+        const f32x4 v = acc[mb];
+        const uint32_t h = pack2<T>(silu(v[0]) * v[2], silu(v[1]) * v[3]);
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)m * p.ldo + (n >> 1)) = h;
+      }
+    }
+  } else {
+    lds_barrier();   // the A chunk buffer is reused for the argmax exchange
+    unsigned long long* sk = reinterpret_cast<unsigned long long*>(sa);   // [16 (wave, g)][64 rows]
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = m0 + mb * 16 + col;
+      const f32x4 v = acc[mb];
+      if (p.out && m < p.M && n < p.N)
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (size_t)m * p.ldo + n) = v;
+      unsigned long long best = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < p.N) best = max(best, argmax_key(v[i], n + i));
+      sk[(wave * 4 + g) * 64 + mb * 16 + col] = best;
+    }
+    lds_barrier();
+    if (tid < 64 && p.keys && m0 + tid < p.M) {
+      unsigned long long best = sk[tid];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) best = max(best, sk[j * 64 + tid]);
+      p.keys[(size_t)blockIdx.x * p.M + m0 + tid] = best;
+    }
+  }
+}
+
+#define TV_LINEAR_CASE(T)                                                                           \
+  switch (epi) {                                                                                    \
+    case kEpiPartial: hipLaunchKernelGGL((linear_kernel<T, kEpiPartial>), grid, dim3(256), 0, s, p); \
+      break;                                                                                        \
+    case kEpiSwiglu: hipLaunchKernelGGL((linear_kernel<T, kEpiSwiglu>), grid, dim3(256), 0, s, p);   \
+      break;                                                                                        \
+    default: hipLaunchKernelGGL((linear_kernel<T, kEpiLogits>), grid, dim3(256), 0, s, p);           \
+  }
+
+void launch_linear(const LinearParams& p, int epi, int dtype, hipStream_t s) {
+  const dim3 grid((p.N + kLinBN - 1) / kLinBN, (p.K + p.k_split - 1) / p.k_split, (p.M + kLinBM - 1) / kLinBM);
+  if (dtype == kF16) {
+    TV_LINEAR_CASE(_Float16)
+  } else {
+    TV_LINEAR_CASE(__bf16)
+  }
+}
+
+// ---------------------------------------------------------------------------
+// residual add + RMSNorm
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
+  __shared__ float red[4];
+  const int m = blockIdx.x;
+  float* x = p.x + (size_t)m * p.dim;
+  int tok = 0;
+  if (p.emb) tok = min(max(p.tokens[m], 0), p.vocab - 1);
+  float ss = 0.0f;
+  for (int k = 4 * threadIdx.x; k < p.dim; k += 1024) {
+    f32x4 v;
+    if (p.emb) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const T*>(p.emb) + (size_t)tok * p.dim + k);
+      float e0, e1, e2, e3;
+      unpack2<T>(w[0], e0, e1);
+      unpack2<T>(w[1], e2, e3);
+      v = f32x4{e0, e1, e2, e3};
+    } else {
+      v = *reinterpret_cast<const f32x4*>(x + k);
+    }
+    if (p.part) {
+      for (int s = 0; s < p.splits; ++s)
+        v += *reinterpret_cast<const f32x4*>(p.part + ((size_t)s * p.M + m) * p.dim + k);
+    }
+    if (p.emb || p.part) *reinterpret_cast<f32x4*>(x + k) = v;
+    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  }
+  ss = group_sum<64>(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)p.dim + p.eps);
+  for (int k = 4 * threadIdx.x; k < p.dim; k += 1024) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(x + k);
+    const f32x4 w = *reinterpret_cast<const f32x4*>(p.weight + k);
+    const u32x2 h = u32x2{pack2<T>(v[0] * r * w[0], v[1] * r * w[1]), pack2<T>(v[2] * r * w[2], v[3] * r * w[3])};
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.xh) + (size_t)m * p.dim + k) = h;
+  }
+}
+
+void launch_norm(const NormParams& p, int dtype, hipStream_t s) {
+  if (dtype == kF16)
+    hipLaunchKernelGGL(norm_kernel<_Float16>, dim3(p.M), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(norm_kernel<__bf16>, dim3(p.M), dim3(256), 0, s, p);
+}
+
+// ---------------------------------------------------------------------------
+// QKV: split reduction, RoPE, q store, K/V cache write
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(256) qkv_rope_kernel(const QKVParams p) {
+  const int qn = p.Hq * p.D;
+  const int kn = p.Hkv * p.D;
+  const int N = qn + 2 * kn;
+  const int half = N >> 1;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)p.M * half) return;
+  const int m = (int)(t / half);
+  const int n = 2 * (int)(t - (long long)m * half);
+  float v0 = 0.0f, v1 = 0.0f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float2 pv = *reinterpret_cast<const float2*>(p.part + ((size_t)s * p.M + m) * N + n);
+    v0 += pv.x;
+    v1 += pv.y;
+  }
+  const int pos = p.positions ? p.positions[m] : p.pos_base + m;
+  if (n < qn + kn) {
+    const int i = (n % p.D) >> 1;
+    const int pr = min(max(pos, 0), p.rope_len - 1);
+    const float2 cs = *reinterpret_cast<const float2*>(p.rope + ((size_t)pr * (p.D >> 1) + i) * 2);
+    const float a = v0 * cs.x - v1 * cs.y;
+    const float b = v0 * cs.y + v1 * cs.x;
+    v0 = a;
+    v1 = b;
+  }
+  const uint32_t packed = pack2<T>(v0, v1);
+  if (n < qn) {
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.q) + (size_t)m * qn + n) = packed;
+    return;
+  }
+  const bool is_k = n < qn + kn;
+  const int e = is_k ? n - qn : n - qn - kn;
+  void* stage = is_k ? p.k_out : p.v_out;
+  if (stage) *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(stage) + (size_t)m * kn + e) = packed;
+  void* cache = is_k ? p.k_cache : p.v_cache;
+  const bool report = is_k && e == 0;   // one thread per row reports the slot
+  if (!p.block_tables || (!cache && !(report && (p.slots || p.err_count)))) return;
+  long long slot = -1;
+  if (pos >= 0 && pos / p.block_size < p.bt_width) {
+    const int blk = p.block_tables[(size_t)m * p.bt_row_step + pos / p.block_size];
+    if (blk >= 0 && blk < p.num_blocks) slot = (long long)blk * p.block_size + pos % p.block_size;
+  }
+  if (cache && slot >= 0)
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(cache) + (size_t)slot * kn + e) = packed;
+  if (report) {
+    if (p.slots) p.slots[m] = (int)slot;
+    if (slot < 0 && p.err_count) atomicAdd(p.err_count, 1u);
+  }
+}
+
+void launch_qkv_rope(const QKVParams& p, int dtype, hipStream_t s) {
+  const long long pairs = (long long)p.M * ((p.Hq + 2 * p.Hkv) * p.D / 2);
+  const dim3 grid((unsigned)((pairs + 255) / 256));
+  if (dtype == kF16)
+    hipLaunchKernelGGL(qkv_rope_kernel<_Float16>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(qkv_rope_kernel<__bf16>, grid, dim3(256), 0, s, p);
+}
+
+__global__ void rope_table_kernel(float* table, int max_pos, int head_dim, float theta) {
+  const int half = head_dim >> 1;
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long long)max_pos * half) return;
+  const int pos = (int)(idx / half);
+  const int i = (int)(idx - (long long)pos * half);
+  const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+  const float ang = (float)pos * freq;
+  table[2 * idx] = cosf(ang);
+  table[2 * idx + 1] = sinf(ang);
+}
+
+void launch_rope_table(float* table, int max_pos, int head_dim, float theta, hipStream_t s) {
+  const long long n = (long long)max_pos * (head_dim / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, table, max_pos,
+                     head_dim, theta);
+}
+
+// ---------------------------------------------------------------------------
+// greedy sampling + position advance
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(64) advance_kernel(const AdvanceParams p) {
+  const int m = blockIdx.x;
+  const int lane = threadIdx.x;
+  unsigned long long best = 0;
+  for (int j = lane; j < p.nparts; j += 64) best = max(best, p.keys[(size_t)j * p.M + m]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ off) << 2, (int)(uint32_t)best);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ off) << 2, (int)(uint32_t)(best >> 32));
+    best = max(best, ((unsigned long long)hi << 32) | lo);
+  }
+  if (lane != 0) return;
+  const int tok = (int)(0xFFFFFFFFu - (uint32_t)best);
+  p.tokens[m] = tok;
+  if (p.positions) {
+    const int pos = p.positions[m];
+    if (p.history && pos >= 0 && pos + 1 < p.history_len) p.history[(size_t)m * p.history_len + pos + 1] = tok;
+    p.positions[m] = pos + 1;
+  }
+  if (p.context_lens) p.context_lens[m] += 1;
+}
+
+void launch_advance(const AdvanceParams& p, hipStream_t s) {
+  hipLaunchKernelGGL(advance_kernel, dim3(p.M), dim3(64), 0, s, p);
+}
+
+}  // namespace tv

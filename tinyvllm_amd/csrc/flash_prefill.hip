@@ -28,22 +28,6 @@ namespace tv {
 // MFMA kernel
 // ---------------------------------------------------------------------------
 
-template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
-template <> __device__ __forceinline__ f32x4 mfma16x16x32<_Float16>(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-template <> __device__ __forceinline__ f32x4 mfma16x16x32<__bf16>(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
-template <> __device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
-  return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
-}
-template <> __device__ __forceinline__ uint32_t pack2<__bf16>(float a, float b) {
-  return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
-}
-
 // max over the four lanes l, l^16, l^32, l^48 (one query column of the S^T
 // accumulator) with gfx950 row / half-wave swaps (VALU, no LDS round trip).
 __device__ __forceinline__ float max_over_g(float x) {

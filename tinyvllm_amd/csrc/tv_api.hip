@@ -8,11 +8,14 @@
 
 #include "../../include/tv_attn.h"
 #include "paged_decode_inst.h"
+#include "tv_error.h"
 #include "tv_params.h"
 
-namespace {
+namespace tv {
 
+namespace {
 thread_local std::string g_err;
+}
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -34,6 +37,16 @@ int check_launch(const char* what) {
   if (e != hipSuccess) return fail(TV_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
   return ok();
 }
+
+const char* last_error() { return g_err.c_str(); }
+
+}  // namespace tv
+
+namespace {
+
+using tv::check_launch;
+using tv::fail;
+using tv::ok;
 
 bool valid_dtype(int d) { return d == TV_F32 || d == TV_F16 || d == TV_BF16; }
 int elem_size(int d) { return d == TV_F32 ? 4 : 2; }
@@ -66,9 +79,9 @@ int vec_width(std::initializer_list<long long> sizes, std::initializer_list<cons
 
 extern "C" {
 
-int tv_abi_version(void) { return 2; }
+int tv_abi_version(void) { return 3; }
 
-const char* tv_last_error(void) { return g_err.c_str(); }
+const char* tv_last_error(void) { return tv::last_error(); }
 
 size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_blocks,
                                        int block_size, int partition_size) {

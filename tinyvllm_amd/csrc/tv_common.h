@@ -98,6 +98,26 @@ __device__ __forceinline__ void store_as(void* base, size_t idx, float v, int dt
   }
 }
 
+// ---- MFMA ------------------------------------------------------------------
+// v_mfma_f32_16x16x32_{f16,bf16}: D = A B + C with A 16x32, B 32x16.  Lane l
+// supplies A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16], j = 0..7, as
+// eight packed elements; it receives D[4 (l / 16) + i][l % 16], i = 0..3.
+template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mfma16x16x32<_Float16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma16x16x32<__bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+}
+template <> __device__ __forceinline__ uint32_t pack2<__bf16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
+}
+
 // ---- wave64 cross-lane helpers ---------------------------------------------
 // DPP controls (GFX9 encoding): quad_perm, row_half_mirror, row_mirror.
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
