@@ -284,6 +284,15 @@ def max_err(got, want):
     return float(np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64)).max())
 
 
+def check_caches(kv, rk, rv):
+    """fp16 caches vs the oracle's: a few fp16 ulps of the largest entry (layer-0
+    rounding differences propagate into the later layers' k/v)."""
+    for layer, (k, v) in enumerate(zip(rk, rv)):
+        for got, want in ((kv.k_cache[layer], k), (kv.v_cache[layer], v)):
+            bound = 4e-3 * max(1.0, float(np.abs(want).max()))
+            assert max_err(got.float().cpu().numpy(), want) < bound, layer
+
+
 def test_prefill_matches_oracle():
     cfg = small_config()
     model, kv, bm, ref, rk, rv = build(cfg)
@@ -295,9 +304,7 @@ def test_prefill_matches_oracle():
         want = ref.prefill(toks, rk, rv, np.array(bm.get_block_table(sid)), 0, 16)
         assert max_err(logits, want) < TOL, sid
         assert bm.get_context_length(sid) == n
-    for layer in range(cfg.n_layers):
-        assert max_err(kv.k_cache[layer].float().cpu().numpy(), rk[layer]) < 4e-3
-        assert max_err(kv.v_cache[layer].float().cpu().numpy(), rv[layer]) < 4e-3
+    check_caches(kv, rk, rv)
 
 
 def prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg):
@@ -312,17 +319,26 @@ def prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg):
     return nxt
 
 
+# (dim, n_heads, n_kv_heads): head_dim 32 takes the unfused path (qkv_rope +
+# tv_paged_decode); head_dim 64 / 128 the fused MFMA step attention, with
+# 2, 8 and 16 query heads per KV head
+DECODE_SHAPES = [(128, 4, 2), (256, 4, 2), (512, 8, 1), (1024, 16, 1), (256, 2, 1)]
+
+
+@pytest.mark.parametrize("shape", DECODE_SHAPES, ids=lambda s: f"dim{s[0]}-h{s[1]}-kv{s[2]}")
 @pytest.mark.parametrize("write_before_attend", [True, False])
-def test_decode_steps_match_oracle(write_before_attend):
+def test_decode_steps_match_oracle(write_before_attend, shape):
     """Engine convention (context = position + 1, engine.py:251) over several steps,
-    teacher-forced with the oracle's greedy tokens."""
-    cfg = small_config()
+    teacher-forced with the oracle's greedy tokens; one context spans every wave
+    of the fused kernel."""
+    dim, nh, nkv = shape
+    cfg = small_config(dim=dim, n_heads=nh, n_kv_heads=nkv, max_seq_len=512)
     model, kv, bm, ref, rk, rv = build(cfg, seed=3, write_before_attend=write_before_attend)
     rng = np.random.default_rng(21)
-    lens = [7, 16, 30, 1]
+    lens = [7, 16, 300, 1]
     toks = prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg)
     jit = model.create_jit_decode(16)
-    max_blocks = 4
+    max_blocks = 20
     for step in range(4):
         pos = [bm.seq_positions[s] for s in range(len(lens))]
         for s, p in enumerate(pos):
@@ -338,8 +354,7 @@ def test_decode_steps_match_oracle(write_before_attend):
         assert logits.shape == (len(lens), 1, cfg.vocab_size)
         assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
         toks = [int(t) for t in greedy_ref(want)]
-    for layer in range(cfg.n_layers):
-        assert max_err(kv.k_cache[layer].float().cpu().numpy(), rk[layer]) < 4e-3
+    check_caches(kv, rk, rv)
 
 
 def test_graph_replay_is_deterministic_and_equals_eager():

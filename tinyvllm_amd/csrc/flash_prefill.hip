@@ -28,21 +28,6 @@ namespace tv {
 // MFMA kernel
 // ---------------------------------------------------------------------------
 
-// max over the four lanes l, l^16, l^32, l^48 (one query column of the S^T
-// accumulator) with gfx950 row / half-wave swaps (VALU, no LDS round trip).
-__device__ __forceinline__ float max_over_g(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
-  x = fmaxf(u32_as_f32(a[0]), u32_as_f32(a[1]));
-  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
-  return fmaxf(u32_as_f32(b[0]), u32_as_f32(b[1]));
-}
-__device__ __forceinline__ float sum_over_g(float x) {
-  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
-  x = u32_as_f32(a[0]) + u32_as_f32(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
-  return u32_as_f32(b[0]) + u32_as_f32(b[1]);
-}
-
 __device__ __forceinline__ int prefill_head(int x, int num_heads, int remap) {
   // Work-groups are dealt to the 8 XCDs round-robin by linear id; with the head
   // on grid.x, id % 8 == x % 8.  Mapping x -> (x % 8) * (Hq / 8) + x / 8 puts

@@ -161,76 +161,119 @@ struct LayerIO {
   int ks_qkv, ks_o, ks_2;
 };
 
-int run_layers(const tv_llama_model* m, const tv_llama_cache* c, const LayerIO& io, hipStream_t s) {
+// Split sum + RoPE + K/V write + attention of one decode layer in one kernel.
+int attend_fused(const tv_llama_model* m, const tv_llama_cache* c, const LayerIO& io, int l, hipStream_t s) {
+  const int dt = m->dtype;
+  const float scale = 1.0f / std::sqrt((float)m->head_dim);
+  const int M = io.M;
+  const tv_llama_decode_args* a = io.dargs;
+  tv::StepAttnParams sp{};
+  sp.out = io.attn;
+  sp.part = io.part;
+  sp.splits = splits_of(m->dim, io.ks_qkv);
+  sp.positions = a->positions;
+  sp.context_lens = a->context_lens;
+  sp.rope = m->rope;
+  sp.rope_len = m->rope_len;
+  sp.k_cache = c->k_caches[l];
+  sp.v_cache = c->v_caches[l];
+  sp.block_tables = a->block_tables;
+  sp.bt_stride = a->bt_stride;
+  sp.max_blocks = a->max_blocks;
+  sp.block_size = c->block_size;
+  sp.num_blocks = c->num_blocks;
+  sp.B = M;
+  sp.Hq = m->n_heads;
+  sp.Hkv = m->n_kv_heads;
+  sp.scale = scale;
+  sp.write_before = a->write_before_attend ? 1 : 0;
+  tv::launch_step_attn(sp, m->head_dim, dt, s);
+  return check_launch("step_attn");
+}
+
+// The same without the fused kernel: qkv_rope, then tv_paged_decode (decode)
+// or tv_flash_prefill (prefill).  In the reference's order the decode stages
+// k/v with their slots and writes them after attention.
+int attend_unfused(const tv_llama_model* m, const tv_llama_cache* c, const LayerIO& io, int l, hipStream_t s) {
   const int dt = m->dtype;
   const int qd = m->n_heads * m->head_dim;
   const int kd = m->n_kv_heads * m->head_dim;
-  const int nqkv = qkv_width(m);
   const float scale = 1.0f / std::sqrt((float)m->head_dim);
   const int M = io.M;
-  for (int l = 0; l < m->n_layers; ++l) {
-    linear(io.xh, m->wqkv[l], M, nqkv, m->dim, m->dim, io.ks_qkv, tv::kEpiPartial, io.part, 0, nullptr, dt, s);
-
-    tv::QKVParams qp{};
-    qp.q = io.q;
-    qp.part = io.part;
-    qp.splits = splits_of(m->dim, io.ks_qkv);
-    qp.rope = m->rope;
-    qp.rope_len = m->rope_len;
-    qp.block_size = c->block_size;
-    qp.num_blocks = c->num_blocks;
-    qp.M = M;
-    qp.Hq = m->n_heads;
-    qp.Hkv = m->n_kv_heads;
-    qp.D = m->head_dim;
-    if (io.decode) {
-      const tv_llama_decode_args* a = io.dargs;
-      qp.positions = a->positions;
-      qp.block_tables = a->block_tables;
-      qp.bt_row_step = a->bt_stride;
-      qp.bt_width = a->bt_stride;
-      if (a->write_before_attend) {
-        qp.k_cache = c->k_caches[l];
-        qp.v_cache = c->v_caches[l];
-      } else {
-        // reference order: stage k/v and their slots now, write them after attention
-        qp.k_out = io.kst;
-        qp.v_out = io.vst;
-        qp.slots = io.slots;
-      }
-    } else {
-      const tv_llama_prefill_args* a = io.pargs;
-      qp.pos_base = a->start_pos;
-      qp.block_tables = a->block_table;
-      qp.bt_row_step = 0;
-      qp.bt_width = a->bt_width;
-      qp.k_out = io.kst;
-      qp.v_out = io.vst;
+  tv::QKVParams qp{};
+  qp.q = io.q;
+  qp.part = io.part;
+  qp.splits = splits_of(m->dim, io.ks_qkv);
+  qp.rope = m->rope;
+  qp.rope_len = m->rope_len;
+  qp.block_size = c->block_size;
+  qp.num_blocks = c->num_blocks;
+  qp.M = M;
+  qp.Hq = m->n_heads;
+  qp.Hkv = m->n_kv_heads;
+  qp.D = m->head_dim;
+  if (io.decode) {
+    const tv_llama_decode_args* a = io.dargs;
+    qp.positions = a->positions;
+    qp.block_tables = a->block_tables;
+    qp.bt_row_step = a->bt_stride;
+    qp.bt_width = a->bt_stride;
+    if (a->write_before_attend) {
       qp.k_cache = c->k_caches[l];
       qp.v_cache = c->v_caches[l];
-    }
-    tv::launch_qkv_rope(qp, dt, s);
-    int rc = check_launch("qkv_rope");
-    if (rc != TV_OK) return rc;
-
-    if (io.decode) {
-      const tv_llama_decode_args* a = io.dargs;
-      rc = tv_paged_decode(io.attn, io.q, c->k_caches[l], c->v_caches[l], a->block_tables, a->context_lens,
-                           a->batch, m->n_heads, m->n_kv_heads, m->head_dim, c->block_size, c->num_blocks,
-                           a->bt_stride, a->max_blocks, scale, dt, dt, a->partition_size, io.attn_ws,
-                           io.attn_ws_bytes, s);
-      if (rc != TV_OK) return rc;
-      if (!a->write_before_attend) {
-        // Llama.decode writes k/v at get_slot() after the JIT call (llama.py:381-386)
-        rc = tv_reshape_and_cache(c->k_caches[l], c->v_caches[l], io.kst, io.vst, io.slots, M, m->n_kv_heads,
-                                  m->head_dim, c->block_size, c->num_blocks, kd, kd, dt, nullptr, s);
-        if (rc != TV_OK) return rc;
-      }
     } else {
-      rc = tv_flash_prefill(io.attn, io.q, io.kst, io.vst, M, M, m->n_heads, m->n_kv_heads, m->head_dim,
-                            m->head_dim, qd, kd, kd, qd, 1, scale, dt, dt, 0, nullptr, 0, s);
+      // reference order: stage k/v and their slots now, write them after attention
+      qp.k_out = io.kst;
+      qp.v_out = io.vst;
+      qp.slots = io.slots;
+    }
+  } else {
+    const tv_llama_prefill_args* a = io.pargs;
+    qp.pos_base = a->start_pos;
+    qp.block_tables = a->block_table;
+    qp.bt_row_step = 0;
+    qp.bt_width = a->bt_width;
+    qp.k_out = io.kst;
+    qp.v_out = io.vst;
+    qp.k_cache = c->k_caches[l];
+    qp.v_cache = c->v_caches[l];
+  }
+  tv::launch_qkv_rope(qp, dt, s);
+  int rc = check_launch("qkv_rope");
+  if (rc != TV_OK) return rc;
+
+  if (io.decode) {
+    const tv_llama_decode_args* a = io.dargs;
+    rc = tv_paged_decode(io.attn, io.q, c->k_caches[l], c->v_caches[l], a->block_tables, a->context_lens,
+                         a->batch, m->n_heads, m->n_kv_heads, m->head_dim, c->block_size, c->num_blocks,
+                         a->bt_stride, a->max_blocks, scale, dt, dt, a->partition_size, io.attn_ws,
+                         io.attn_ws_bytes, s);
+    if (rc != TV_OK) return rc;
+    if (!a->write_before_attend) {
+      // Llama.decode writes k/v at get_slot() after the JIT call (llama.py:381-386)
+      rc = tv_reshape_and_cache(c->k_caches[l], c->v_caches[l], io.kst, io.vst, io.slots, M, m->n_kv_heads,
+                                m->head_dim, c->block_size, c->num_blocks, kd, kd, dt, nullptr, s);
       if (rc != TV_OK) return rc;
     }
+  } else {
+    rc = tv_flash_prefill(io.attn, io.q, io.kst, io.vst, M, M, m->n_heads, m->n_kv_heads, m->head_dim,
+                          m->head_dim, qd, kd, kd, qd, 1, scale, dt, dt, 0, nullptr, 0, s);
+    if (rc != TV_OK) return rc;
+  }
+  return TV_OK;
+}
+
+int run_layers(const tv_llama_model* m, const tv_llama_cache* c, const LayerIO& io, hipStream_t s) {
+  const int dt = m->dtype;
+  const int qd = m->n_heads * m->head_dim;
+  const int nqkv = qkv_width(m);
+  const int M = io.M;
+  const bool fused_attn =
+      io.decode && tv::step_attn_supported(m->head_dim, m->n_heads / m->n_kv_heads, c->block_size);
+  for (int l = 0; l < m->n_layers; ++l) {
+    linear(io.xh, m->wqkv[l], M, nqkv, m->dim, m->dim, io.ks_qkv, tv::kEpiPartial, io.part, 0, nullptr, dt, s);
+    int rc = fused_attn ? attend_fused(m, c, io, l, s) : attend_unfused(m, c, io, l, s);
+    if (rc != TV_OK) return rc;
 
     linear(io.attn, m->wo[l], M, m->dim, qd, qd, io.ks_o, tv::kEpiPartial, io.part, 0, nullptr, dt, s);
     norm(io.x, io.xh, io.part, splits_of(qd, io.ks_o), nullptr, nullptr, 0, m->ffn_norm[l], M, m->dim, m->norm_eps,

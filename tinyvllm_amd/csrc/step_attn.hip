@@ -1,0 +1,309 @@
+// Attention of the batched decode step (gfx950), fused with the end of the
+// q|k|v projection.  One work-group per (sequence, KV head):
+//  1. sums the split-K partials of the fused projection for the G = Hq/Hkv
+//     query heads of the group and for k, v, and rotates q and k
+//     (apply_rope, llama.py:34-55);
+//  2. writes k, v into the cache slot of the position -- before attention, or
+//     after it in the reference's order (llama.py:378-386);
+//  3. attends over the cached context on MFMA: S^T = K Q^T with the group's
+//     query heads as the 16 columns (heads >= G are zero), an online softmax
+//     over 32-token tiles, O^T += V^T P^T with P kept in registers as the B
+//     operand and V^T staged per wave in LDS;
+//  4. merges the waves' (max, sum, O) in LDS and stores the G output rows.
+// With 8 query heads per KV head at head_dim 64, scores and P.V cost 4
+// multiply-adds per cached byte: more than the VALU delivers at HBM speed on
+// MI355X (a wave64 fp32 FMA occupies a SIMD for 4 cycles), so this kernel
+// runs them on the matrix cores and stays bound by the K/V stream.  Semantics
+// are those of paged_decode_attention (llama.py:97-144): softmax over the first
+// context_len cached positions (all table positions when context_len <= 0),
+// scale 1/sqrt(D), query head h on KV head h / G.
+#include "tv_common.h"
+#include "tv_dense.h"
+
+namespace tv {
+
+template <typename T, int D, int NW>
+__global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams p) {
+  constexpr int KS = D / 32;        // MFMA k steps over the head dim
+  constexpr int DB = D / 16;        // 16-dim blocks of O^T
+  constexpr int VP = 32 + 4;        // LDS pitch (tokens) of a wave's V^T tile: 8-byte reads of 16 rows hit distinct banks
+  constexpr int VU = D / 32;        // (token pair, 8-dim chunk) V units per lane per tile
+  constexpr int SVT = NW * D * VP;  // V^T tiles of all waves (elements)
+  constexpr int SO = NW * 16 * D * 2;   // merge buffer [NW][16][D] floats, in elements
+  constexpr int UNION = SVT > SO ? SVT : SO;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[16 * D + UNION];
+  __shared__ uint32_t snew[D];      // k (D/2 words) then v, for the write after attention
+  __shared__ float sm[NW][16];
+  __shared__ float sl[NW][16];
+  uint16_t* sq = smem;                       // [16 heads][D] query rows, heads >= G zero
+  uint16_t* svt = smem + 16 * D;
+
+  const int kvh = blockIdx.x;
+  const int b = blockIdx.y;
+  const int G = p.Hq / p.Hkv;
+  const int N = (p.Hq + 2 * p.Hkv) * D;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int bs = p.block_size;
+  const int width = p.max_blocks * bs;
+  const int ctx = p.context_lens[b];
+  const int len = ctx <= 0 ? width : min(ctx, width);
+  const int* bt = p.block_tables + (size_t)b * p.bt_stride;
+  const int pos = p.positions[b];
+  long long slot = -1;
+  if (pos >= 0 && pos / bs < p.bt_stride) {
+    const int blk = bt[pos / bs];
+    if (blk >= 0 && blk < p.num_blocks) slot = (long long)blk * bs + pos % bs;
+  }
+  const size_t rs = (size_t)p.Hkv * D;   // elements between cache rows
+  T* kcache = reinterpret_cast<T*>(p.k_cache) + (size_t)kvh * D;
+  T* vcache = reinterpret_cast<T*>(p.v_cache) + (size_t)kvh * D;
+
+  // ---- q, k, v of the new token -----------------------------------------
+  {
+    const int nq = G * (D / 2);
+    const int pr = min(max(pos, 0), p.rope_len - 1);
+    const float* part = p.part + (size_t)b * N;
+    const size_t sstride = (size_t)p.B * N;
+    for (int it = tid; it < nq + D; it += 64 * NW) {
+      int n, d2;
+      if (it < nq) {
+        d2 = it % (D / 2);
+        n = (kvh * G + it / (D / 2)) * D + 2 * d2;
+      } else if (it < nq + D / 2) {
+        d2 = it - nq;
+        n = p.Hq * D + kvh * D + 2 * d2;
+      } else {
+        d2 = it - nq - D / 2;
+        n = (p.Hq + p.Hkv) * D + kvh * D + 2 * d2;
+      }
+      float v0 = 0.0f, v1 = 0.0f;
+      for (int s = 0; s < p.splits; ++s) {
+        const float2 pv = *reinterpret_cast<const float2*>(part + s * sstride + n);
+        v0 += pv.x;
+        v1 += pv.y;
+      }
+      if (it < nq + D / 2) {
+        const float2 cs = *reinterpret_cast<const float2*>(p.rope + ((size_t)pr * (D / 2) + d2) * 2);
+        const float a = v0 * cs.x - v1 * cs.y;
+        const float c2 = v0 * cs.y + v1 * cs.x;
+        v0 = a;
+        v1 = c2;
+      }
+      const uint32_t w = pack2<T>(v0, v1);
+      if (it < nq) {
+        *reinterpret_cast<uint32_t*>(&sq[(it / (D / 2)) * D + 2 * d2]) = w;
+      } else if (p.write_before) {
+        if (slot >= 0)
+          *reinterpret_cast<uint32_t*>((it < nq + D / 2 ? kcache : vcache) + (size_t)slot * rs + 2 * d2) = w;
+      } else {
+        snew[it - nq] = w;
+      }
+    }
+    for (int it = tid; it < (16 - G) * (D / 2); it += 64 * NW)
+      *reinterpret_cast<uint32_t*>(&sq[G * D + 2 * it]) = 0u;
+  }
+  __syncthreads();   // q rows in LDS; the slot written before any wave reads it
+
+  // ---- attention over [0, len) ----------------------------------------------
+  u32x4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(&sq[col * D + 32 * ks + 8 * g]);
+  const float c = p.scale * kLog2e;
+  float m = kNegInf;
+  float lsum = 0.0f;
+  f32x4 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint16_t* vt = svt + wave * (D * VP);
+  const int ntiles = (len + 31) >> 5;
+  const int nt = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;   // this wave's tiles: wave + NW j
+
+  struct Tile {
+    u32x4 k[2][KS];
+    u32x4 v[VU][2];
+    int t0;
+    bool ok0, ok1;
+  };
+  // Tile j of this wave: tokens t0 .. t0+31, two 16-token halves each inside
+  // one cache block (block_size is a multiple of 16).
+  auto load = [&](int j, Tile& r) {
+    const int t0 = (wave + NW * j) * 32;
+    r.t0 = t0;
+    int b0 = bt[min(t0 / bs, p.max_blocks - 1)];
+    int b1 = bt[min((t0 + 16) / bs, p.max_blocks - 1)];
+    r.ok0 = (unsigned)b0 < (unsigned)p.num_blocks;
+    r.ok1 = (unsigned)b1 < (unsigned)p.num_blocks;
+    b0 = r.ok0 ? b0 : 0;
+    b1 = r.ok1 ? b1 : 0;
+    const size_t base0 = ((size_t)b0 * bs + t0 % bs) * rs;
+    const size_t base1 = ((size_t)b1 * bs + (t0 + 16) % bs) * rs;
+    // K rows: lane (token col of the half, 8-dim group g)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      r.k[0][ks] = *reinterpret_cast<const u32x4*>(kcache + base0 + col * rs + 32 * ks + 8 * g);
+      r.k[1][ks] = *reinterpret_cast<const u32x4*>(kcache + base1 + col * rs + 32 * ks + 8 * g);
+    }
+    // V rows: lane (token pair tp, 8-dim chunk ch)
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int unit = lane + 64 * i;
+      const int tp = unit & 15;
+      const int ch = unit >> 4;
+      const size_t base = (tp < 8 ? base0 : base1) + (size_t)(2 * (tp & 7)) * rs + 8 * ch;
+      r.v[i][0] = *reinterpret_cast<const u32x4*>(vcache + base);
+      r.v[i][1] = *reinterpret_cast<const u32x4*>(vcache + base + rs);
+    }
+  };
+
+  auto consume = [&](const Tile& r) {
+    // S^T: st[tb][i] = q_head(col) . k(token t0 + 16 tb + 4 g + i)
+    f32x4 st[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      st[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) st[tb] = mfma16x16x32<T>(r.k[tb][ks], qf[ks], st[tb]);
+    }
+    const bool partial = r.t0 + 32 > len || !r.ok0 || !r.ok1;
+    if (partial) {
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool ok = r.t0 + 16 * tb + 4 * g + i < len && (tb ? r.ok1 : r.ok0);
+          st[tb][i] = ok ? st[tb][i] : kNegInf;
+        }
+    }
+    float mt = fmaxf(fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3])),
+                     fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3])));
+    mt = max_over_g(mt);
+    // the running max is only raised when it grows by more than 8 log2 units
+    const float mtc = mt * c;
+    float mc = m == kNegInf ? kNegInf : m * c;
+    if (__builtin_amdgcn_ballot_w64(mtc > mc + 8.0f) != 0) {
+      __asm__ volatile("" ::: "memory");
+      const float mn = mtc > mc + 8.0f ? fmaxf(m, mt) : m;
+      const float alpha = mn == kNegInf ? 1.0f : fast_exp2((m - mn) * c);
+      m = mn;
+      mc = m == kNegInf ? kNegInf : m * c;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+    }
+    if (mc == kNegInf) mc = 0.0f;
+    float e[2][4];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[tb][i] = fast_exp2(fmaf(st[tb][i], c, -mc));
+        lsum += e[tb][i];
+      }
+    // reduction index kk = 8 g + j: token 4 g + j of the first half for j < 4,
+    // token 16 + 4 g + j - 4 for j >= 4, on both MFMA operands
+    const u32x4 pf = u32x4{pack2<T>(e[0][0], e[0][1]), pack2<T>(e[0][2], e[0][3]), pack2<T>(e[1][0], e[1][1]),
+                           pack2<T>(e[1][2], e[1][3])};
+    // V^T tile: vt[dim][token] as 32-bit token pairs (rows of masked tokens are zeroed)
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int unit = lane + 64 * i;
+      const int tp = unit & 15;
+      const int ch = unit >> 4;
+      u32x4 v0 = r.v[i][0], v1 = r.v[i][1];
+      if (partial) {
+        const int tok = r.t0 + 2 * tp;
+        const bool okb = tp < 8 ? r.ok0 : r.ok1;
+        if (!okb || tok >= len) v0 = u32x4{0, 0, 0, 0};
+        if (!okb || tok + 1 >= len) v1 = u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint16_t* dst = &vt[(8 * ch + 2 * w) * VP + 2 * tp];
+        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(dst + VP) = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
+      }
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const uint16_t* row = &vt[(db * 16 + col) * VP + 4 * g];
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+      o[db] = mfma16x16x32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, o[db]);
+    }
+  };
+
+  if (nt > 0) {
+    // two tiles in flight; the loads are unconditional (the last tile is
+    // re-read) so the compiler waits for exactly the tile it consumes
+    Tile ta, tb;
+    load(0, ta);
+    load(min(1, nt - 1), tb);
+    int j = 0;
+    for (; j + 1 < nt; j += 2) {
+      consume(ta);
+      load(min(j + 2, nt - 1), ta);
+      consume(tb);
+      load(min(j + 3, nt - 1), tb);
+    }
+    if (j < nt) consume(ta);
+  }
+
+  // ---- merge the waves ----------------------------------------------------------
+  lsum = sum_over_g(lsum);
+  __syncthreads();   // every wave is done with its V^T tile: the buffer becomes [NW][16][D] floats
+  float* so = reinterpret_cast<float*>(svt);
+  if (g == 0) {
+    sm[wave][col] = m;
+    sl[wave][col] = lsum;
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+    *reinterpret_cast<f32x4*>(&so[(wave * 16 + col) * D + db * 16 + 4 * g]) = o[db];
+  __syncthreads();
+  T* out = reinterpret_cast<T*>(p.out) + ((size_t)b * p.Hq + (size_t)kvh * G) * D;
+  for (int it = tid; it < G * D; it += 64 * NW) {
+    const int h = it / D;
+    const int d = it - h * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w][h]);
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = sm[w][h] == kNegInf ? 0.0f : fast_exp2((sm[w][h] - M) * c);
+      L += sl[w][h] * f;
+      acc += so[(w * 16 + h) * D + d] * f;
+    }
+    out[it] = from_float<T>(L > 0.0f ? acc / L : 0.0f);
+  }
+  if (!p.write_before && slot >= 0 && tid < D) {
+    // the reference's order: the step's k/v reach the cache after attention
+    T* dst = (tid < D / 2 ? kcache : vcache) + (size_t)slot * rs + 2 * (tid % (D / 2));
+    *reinterpret_cast<uint32_t*>(dst) = snew[tid];
+  }
+}
+
+bool step_attn_supported(int head_dim, int group, int block_size) {
+  return (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 16 && block_size % 16 == 0;
+}
+
+// Waves per work-group: 8 at head_dim 64 (two per SIMD with one work-group per
+// CU at batch 64 x 4 KV heads); 4 at head_dim 128, whose double-buffered tiles
+// need more than the 256 registers two waves per SIMD allow.
+void launch_step_attn(const StepAttnParams& p, int head_dim, int dtype, hipStream_t s) {
+  const dim3 grid(p.Hkv, p.B);
+  if (dtype == kF16) {
+    if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<_Float16, 64, 8>), grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL((step_attn_kernel<_Float16, 128, 4>), grid, dim3(256), 0, s, p);
+  } else {
+    if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<__bf16, 64, 8>), grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL((step_attn_kernel<__bf16, 128, 4>), grid, dim3(256), 0, s, p);
+  }
+}
+
+}  // namespace tv

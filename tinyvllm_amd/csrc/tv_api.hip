@@ -57,9 +57,13 @@ int ilog2(long long x) {
   return r;
 }
 
-// Largest power of two <= 8 that divides the GQA group.
+#ifndef TV_DECODE_GT_MAX
+#define TV_DECODE_GT_MAX 8
+#endif
+
+// Largest power of two <= TV_DECODE_GT_MAX that divides the GQA group.
 int heads_per_group_chunk(int group) {
-  for (int gt = 8; gt > 1; gt >>= 1)
+  for (int gt = TV_DECODE_GT_MAX; gt > 1; gt >>= 1)
     if (group % gt == 0) return gt;
   return 1;
 }

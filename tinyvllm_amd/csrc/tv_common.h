@@ -118,6 +118,21 @@ template <> __device__ __forceinline__ uint32_t pack2<__bf16>(float a, float b) 
   return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
 }
 
+// max over the four lanes l, l^16, l^32, l^48 (one query column of the S^T
+// accumulator) with gfx950 row / half-wave swaps (VALU, no LDS round trip).
+__device__ __forceinline__ float max_over_g(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  x = fmaxf(u32_as_f32(a[0]), u32_as_f32(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  return fmaxf(u32_as_f32(b[0]), u32_as_f32(b[1]));
+}
+__device__ __forceinline__ float sum_over_g(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  x = u32_as_f32(a[0]) + u32_as_f32(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x), false, false);
+  return u32_as_f32(b[0]) + u32_as_f32(b[1]);
+}
+
 // ---- wave64 cross-lane helpers ---------------------------------------------
 // DPP controls (GFX9 encoding): quad_perm, row_half_mirror, row_mirror.
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]

@@ -72,6 +72,29 @@ struct AdvanceParams {
   int history_len;
 };
 
+// Decode-step attention fused with the q|k|v split sum, RoPE and the K/V write
+// (step_attn.hip); grid (Hkv, B).
+struct StepAttnParams {
+  void* out;              // [B, Hq, D] T
+  const float* part;      // [splits, B, (Hq+2Hkv)*D] q|k|v projection partials
+  int splits;
+  const int* positions;   // [B]
+  const int* context_lens;   // [B]
+  const float* rope;      // [rope_len, D/2, 2]
+  int rope_len;
+  void* k_cache;          // [NB, bs, Hkv, D] T
+  void* v_cache;
+  const int* block_tables;   // [B, bt_stride]
+  int bt_stride, max_blocks;
+  int block_size, num_blocks;
+  int B, Hq, Hkv;
+  float scale;
+  int write_before;       // 1: k/v written before attention; 0: after (the reference's order)
+};
+
+bool step_attn_supported(int head_dim, int group, int block_size);
+void launch_step_attn(const StepAttnParams& p, int head_dim, int dtype, hipStream_t s);
+
 void launch_linear(const LinearParams& p, int epilogue, int dtype, hipStream_t s);
 void launch_norm(const NormParams& p, int dtype, hipStream_t s);
 void launch_qkv_rope(const QKVParams& p, int dtype, hipStream_t s);

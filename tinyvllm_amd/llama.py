@@ -193,6 +193,8 @@ class Llama:
             raise ValueError("n_heads must be a multiple of n_kv_heads and hidden_dim even")
         self.config = config
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.write_before_attend = bool(write_before_attend)
         self.rope_len = config.max_seq_len * 2          # llama.py:258
         self.rope = torch.empty((self.rope_len, config.head_dim // 2, 2), dtype=torch.float32, device=self.device)
@@ -266,29 +268,43 @@ class Llama:
     def prefill(self, tokens, kv_cache, block_manager, seq_id, start_pos=0, *, logits="all"):
         """Prompt pass of one sequence (llama.py:264-285).  Returns logits
         [1, L, vocab] float32 (``logits="last"``: [1, 1, vocab]; ``None``: no logits)."""
+        toks = _i32(tokens, self.device).reshape(-1)
+        n = toks.numel()
+        for pos in range(start_pos, start_pos + n):            # llama.py:206, at layer 0
+            block_manager.ensure_block_for_position(seq_id, pos)
+        out = self.prefill_table(toks, kv_cache, block_manager.get_block_table(seq_id), start_pos, logits=logits)
+        for _ in range(n):                                     # llama.py:282-283
+            block_manager.advance_position(seq_id)
+        return out
+
+    def prefill_table(self, tokens, kv_cache, block_table, start_pos=0, *, logits="all", next_token=None):
+        """Prompt pass over an explicit block table (the table must cover every
+        position).  ``next_token``: an int32 device tensor slice that receives the
+        greedy token after the last position."""
         c = self.config
         toks = _i32(tokens, self.device).reshape(-1)
         n = toks.numel()
         if n == 0:
             raise ValueError("prefill needs at least one token")
-        for pos in range(start_pos, start_pos + n):            # llama.py:206, at layer 0
-            block_manager.ensure_block_for_position(seq_id, pos)
-        table = _i32(block_manager.get_block_table(seq_id), self.device)
+        table = _i32(block_table, self.device).reshape(-1)
+        if (start_pos + n - 1) // kv_cache.block_size >= table.numel():
+            raise ValueError("block table does not cover the prompt")
         lib = _lib.load()
         need = lib.tv_llama_prefill_workspace_bytes(ctypes.byref(self._model), n)
         if self._prefill_ws is None or self._prefill_ws.numel() < need:
             self._prefill_ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         rows = 0 if logits is None else (1 if logits == "last" else n)
         out = torch.empty((1, rows, c.vocab_size), dtype=torch.float32, device=self.device) if rows else None
+        if next_token is not None and (next_token.dtype != torch.int32 or next_token.device != self.device):
+            raise ValueError("next_token must be an int32 tensor on the model's device")
         cache, keep = self.cache_struct(kv_cache)
         args = _PrefillArgs(n, toks.data_ptr(), start_pos, table.data_ptr(), table.numel(),
-                            out.data_ptr() if out is not None else None, 1 if logits == "last" else 0, None,
+                            out.data_ptr() if out is not None else None, 1 if logits == "last" else 0,
+                            next_token.data_ptr() if next_token is not None else None,
                             self._prefill_ws.data_ptr(), self._prefill_ws.numel())
         _lib.check(lib.tv_llama_prefill(ctypes.byref(self._model), ctypes.byref(cache), ctypes.byref(args),
                                         _lib.stream_ptr(self.device)), "tv_llama_prefill")
         del keep
-        for _ in range(n):                                     # llama.py:282-283
-            block_manager.advance_position(seq_id)
         return out
 
     # ---- decode ------------------------------------------------------------------

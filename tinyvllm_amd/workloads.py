@@ -187,3 +187,50 @@ def config2_prefill_tinyllama(device="cuda", seed=0, lengths=(512, 1024), spare_
         wl.v.append(v)
         wl.host[i] = (hq, hk, hv)
     return wl
+
+
+class E2EWorkload:
+    """Batched greedy decode of a random-init LLaMA model over a prefilled paged cache."""
+
+    def __init__(self, model, kv_cache, tables, prompts, decode_steps, seed):
+        self.model = model
+        self.kv = kv_cache
+        self.tables = tables                  # [B, blocks per sequence] int32, covers prompt + decode
+        self.prompts = prompts                # [B, L] int32
+        self.batch, self.prompt_len = prompts.shape
+        self.decode_steps = decode_steps
+        self.seed = seed
+
+    def weight_bytes_per_step(self):
+        """Weights read by one step: everything but the embedding table, of which only B rows are read."""
+        m = self.model
+        emb = m.tok_embeddings
+        return m.weight_bytes() - emb.numel() * emb.element_size() + self.batch * emb.shape[1] * emb.element_size()
+
+    def kv_bytes(self, ctx):
+        """K and V rows attended by one step at context ctx per sequence, all layers (+ the write)."""
+        c = self.model.config
+        row = c.n_kv_heads * c.head_dim * self.kv.k_cache[0].element_size()
+        return self.batch * c.n_layers * 2 * row * (ctx + 1)
+
+    def bytes_for_steps(self, first_ctx, steps):
+        return sum(self.weight_bytes_per_step() + self.kv_bytes(first_ctx + i) for i in range(steps))
+
+
+def config4_e2e_tinyllama(device="cuda", seed=0, batch=64, prompt_len=1024, decode_steps=128, block_size=16,
+                          pool_margin=0.1):
+    """Random-init TinyLlama-1.1B (fp16 weights ~ N(0, 0.02), unit norms), ``batch``
+    prompts of ``prompt_len`` seeded token ids, blocks for prompt + decode drawn from
+    a shuffled pool sized to the need + 10%."""
+    from .kv_cache import KVCache
+    from .llama import Llama, LlamaConfig
+    cfg = LlamaConfig.tinyllama_1b("float16")
+    model = Llama(cfg, seed=seed, device=device)
+    rng = np.random.Generator(np.random.PCG64(seed))
+    per_seq = -(-(prompt_len + decode_steps) // block_size)
+    num_blocks = int(np.ceil((1 + pool_margin) * batch * per_seq))
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    tables = perm[:batch * per_seq].reshape(batch, per_seq)
+    prompts = rng.integers(0, cfg.vocab_size, (batch, prompt_len)).astype(np.int32)
+    kv = KVCache(cfg.n_layers, num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype, device)
+    return E2EWorkload(model, kv, tables, prompts, decode_steps, seed)
