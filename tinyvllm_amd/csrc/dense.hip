@@ -42,8 +42,12 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int vof
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
+#ifndef TV_LINEAR_MIN_BLOCKS
+#define TV_LINEAR_MIN_BLOCKS 1
+#endif
+
 template <typename T, int EPI>
-__global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
+__global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const LinearParams p) {
   constexpr int KP = kLinKC + 8;   // LDS pitch (elements): 16-byte reads of 16 rows hit distinct banks
   __shared__ __attribute__((aligned(16))) uint16_t sa[kLinBM * KP];
 
@@ -52,11 +56,20 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
   const int lane = tid & 63;
   const int g = lane >> 4;
   const int col = lane & 15;
-  const int n_wave = blockIdx.x * kLinBN + wave * 16;
+  // grid (splits, n tiles, m tiles): consecutive work-groups take different
+  // K splits of one n tile, and each n tile starts its chunk sequence at a
+  // different chunk, so the work-groups in flight read different column
+  // ranges of W.  (With the row pitch of W a power of two, work-groups that
+  // march through the same columns in step all hit the same HBM channels.)
+  const int split = blockIdx.x;
+  const int ntile = blockIdx.y;
+  const int n_wave = ntile * kLinBN + wave * 16;
   const int m0 = blockIdx.z * kLinBM;
-  const int kb = blockIdx.y * p.k_split;
+  const int kb = split * p.k_split;
   const int ke = min(kb + p.k_split, p.K);
   const int nc = (ke - kb + kLinKC - 1) / kLinKC;
+  const int rot = ntile % nc;
+  auto chunk_of = [&](int i) { const int c = i + rot; return c < nc ? c : c - nc; };
 
   // Buffer loads: reads past the end of W (rows >= N) or of A (rows >= M)
   // return zero in hardware, so no address is clamped and every offset inside
@@ -72,8 +85,10 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
 
   // W: lane (row col, k group g) reads 8 elements per 32-wide k step.  Columns
   // past the split are multiplied by zero rows of A.
-  auto loadW = [&](int c, u32x4 (&r)[8]) {
-    const int off = w_voff + c * kLinKC * (int)sizeof(T);
+  // i is the position in this work-group's chunk sequence; positions past the
+  // last chunk re-read it (W) or load zeros (A), so padding steps add nothing.
+  auto loadW = [&](int i, u32x4 (&r)[8]) {
+    const int off = w_voff + chunk_of(min(i, nc - 1)) * kLinKC * (int)sizeof(T);
 #pragma unroll
     for (int s = 0; s < 8; ++s) r[s] = buffer_load16(wres, off + 64 * s, 0);
   };
@@ -81,8 +96,9 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
   // tid % 32 of rows tid / 32 + 8 i.  Columns past the split are zeroed when
   // stored to LDS (not at load time, so the loads stay in flight while the
   // previous chunk computes).
-  auto loadA = [&](int c, u32x4 (&r)[8], bool& valid) {
-    valid = kb + c * kLinKC + 8 * (tid & 31) < ke;
+  auto loadA = [&](int i, u32x4 (&r)[8], bool& valid) {
+    const int c = chunk_of(min(i, nc - 1));
+    valid = i < nc && kb + c * kLinKC + 8 * (tid & 31) < ke;
     const int off = a_voff + c * kLinKC * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = buffer_load16(ares, off, i * a_rows8);
@@ -124,21 +140,27 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
     compute(w0);
   } else {
     // W and A of chunk c + 1 are in flight while chunk c computes.  The loads
-    // are unconditional (the last chunk is re-read) so the compiler can wait
-    // for exactly the chunk it needs.
-    for (int c = 0; c < nc; c += 2) {
-      loadW(min(c + 1, nc - 1), w1);
+    // are unconditional and the step count is padded to even (the padding step
+    // multiplies zero A rows), so the loop body has no exit and the compiler
+    // waits for exactly the chunk it needs.
+    // (sched_barrier keeps each prefetch issued before the waits that follow)
+    const int ncp = (nc + 1) & ~1;
+    for (int c = 0; c < ncp; c += 2) {
+      loadW(c + 1, w1);
+      __builtin_amdgcn_sched_barrier(0);
       lds_barrier();
       storeA(ar, av);
       lds_barrier();
-      loadA(min(c + 1, nc - 1), ar, av);
+      loadA(c + 1, ar, av);
+      __builtin_amdgcn_sched_barrier(0);
       compute(w0);
-      if (c + 1 >= nc) break;
-      loadW(min(c + 2, nc - 1), w0);
+      loadW(c + 2, w0);
+      __builtin_amdgcn_sched_barrier(0);
       lds_barrier();
       storeA(ar, av);
       lds_barrier();
-      loadA(min(c + 2, nc - 1), ar, av);
+      loadA(c + 2, ar, av);
+      __builtin_amdgcn_sched_barrier(0);
       compute(w1);
     }
   }
@@ -150,7 +172,7 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
     for (int mb = 0; mb < 4; ++mb) {
       const int m = m0 + mb * 16 + col;
       if (m < p.M && n < p.N)
-        *reinterpret_cast<f32x4*>(p.part + ((size_t)blockIdx.y * p.M + m) * p.N + n) = acc[mb];
+        *reinterpret_cast<f32x4*>(p.part + ((size_t)split * p.M + m) * p.N + n) = acc[mb];
     }
   } else if constexpr (EPI == kEpiSwiglu) {
     // rows 4j, 4j+1 of W are w1 rows 2j, 2j+1; rows 4j+2, 4j+3 the matching w3 rows
@@ -183,7 +205,7 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
       unsigned long long best = sk[tid];
 #pragma unroll
       for (int j = 1; j < 16; ++j) best = max(best, sk[j * 64 + tid]);
-      p.keys[(size_t)blockIdx.x * p.M + m0 + tid] = best;
+      p.keys[(size_t)ntile * p.M + m0 + tid] = best;
     }
   }
 }
@@ -198,7 +220,7 @@ __global__ void __launch_bounds__(256) linear_kernel(const LinearParams p) {
   }
 
 void launch_linear(const LinearParams& p, int epi, int dtype, hipStream_t s) {
-  const dim3 grid((p.N + kLinBN - 1) / kLinBN, (p.K + p.k_split - 1) / p.k_split, (p.M + kLinBM - 1) / kLinBM);
+  const dim3 grid((p.K + p.k_split - 1) / p.k_split, (p.N + kLinBN - 1) / kLinBN, (p.M + kLinBM - 1) / kLinBM);
   if (dtype == kF16) {
     TV_LINEAR_CASE(_Float16)
   } else {
@@ -210,49 +232,89 @@ void launch_linear(const LinearParams& p, int epi, int dtype, hipStream_t s) {
 // residual add + RMSNorm
 // ---------------------------------------------------------------------------
 
-template <typename T>
+// One work-group per row; thread t holds float4 vectors t + 256 i (VPT of
+// them) in registers, so the row is read once: every load (weight, embedding
+// or residual, split partials) is issued before the first add, one LDS
+// reduction gives the mean square, and the normalised row is written from
+// registers.
+template <typename T, int VPT>
 __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
   __shared__ float red[4];
   const int m = blockIdx.x;
   float* x = p.x + (size_t)m * p.dim;
   int tok = 0;
   if (p.emb) tok = min(max(p.tokens[m], 0), p.vocab - 1);
-  float ss = 0.0f;
-  for (int k = 4 * threadIdx.x; k < p.dim; k += 1024) {
-    f32x4 v;
+  f32x4 v[VPT], w[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int k = min(4 * (threadIdx.x + 256 * i), p.dim - 4);   // clamped: lanes past dim re-read the last vector
+    w[i] = *reinterpret_cast<const f32x4*>(p.weight + k);
     if (p.emb) {
-      const u32x2 w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const T*>(p.emb) + (size_t)tok * p.dim + k);
+      const u32x2 e = *reinterpret_cast<const u32x2*>(reinterpret_cast<const T*>(p.emb) + (size_t)tok * p.dim + k);
       float e0, e1, e2, e3;
-      unpack2<T>(w[0], e0, e1);
-      unpack2<T>(w[1], e2, e3);
-      v = f32x4{e0, e1, e2, e3};
+      unpack2<T>(e[0], e0, e1);
+      unpack2<T>(e[1], e2, e3);
+      v[i] = f32x4{e0, e1, e2, e3};
     } else {
-      v = *reinterpret_cast<const f32x4*>(x + k);
+      v[i] = *reinterpret_cast<const f32x4*>(x + k);
     }
-    if (p.part) {
-      for (int s = 0; s < p.splits; ++s)
-        v += *reinterpret_cast<const f32x4*>(p.part + ((size_t)s * p.M + m) * p.dim + k);
+  }
+  if (p.part) {
+    // four splits per batch of loads; indexes past the last split re-read it and are dropped
+    for (int s0 = 0; s0 < p.splits; s0 += 4) {
+      f32x4 t[4][VPT];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+          const int k = min(4 * (threadIdx.x + 256 * i), p.dim - 4);
+          t[u][i] = *reinterpret_cast<const f32x4*>(p.part + ((size_t)min(s0 + u, p.splits - 1) * p.M + m) * p.dim + k);
+        }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < p.splits) {
+#pragma unroll
+          for (int i = 0; i < VPT; ++i) v[i] += t[u][i];
+        }
     }
-    if (p.emb || p.part) *reinterpret_cast<f32x4*>(x + k) = v;
-    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int k = 4 * (threadIdx.x + 256 * i);
+    if (k < p.dim) {
+      if (p.emb || p.part) *reinterpret_cast<f32x4*>(x + k) = v[i];
+      ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    }
   }
   ss = group_sum<64>(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
+  lds_barrier();
   const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)p.dim + p.eps);
-  for (int k = 4 * threadIdx.x; k < p.dim; k += 1024) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(x + k);
-    const f32x4 w = *reinterpret_cast<const f32x4*>(p.weight + k);
-    const u32x2 h = u32x2{pack2<T>(v[0] * r * w[0], v[1] * r * w[1]), pack2<T>(v[2] * r * w[2], v[3] * r * w[3])};
-    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.xh) + (size_t)m * p.dim + k) = h;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int k = 4 * (threadIdx.x + 256 * i);
+    if (k < p.dim) {
+      const f32x4 a = v[i] * r * w[i];
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.xh) + (size_t)m * p.dim + k) =
+          u32x2{pack2<T>(a[0], a[1]), pack2<T>(a[2], a[3])};
+    }
   }
+}
+
+template <typename T> void launch_norm_t(const NormParams& p, hipStream_t s) {
+  const int vpt = (p.dim + 1023) / 1024;
+  if (vpt <= 1) hipLaunchKernelGGL((norm_kernel<T, 1>), dim3(p.M), dim3(256), 0, s, p);
+  else if (vpt <= 2) hipLaunchKernelGGL((norm_kernel<T, 2>), dim3(p.M), dim3(256), 0, s, p);
+  else if (vpt <= 4) hipLaunchKernelGGL((norm_kernel<T, 4>), dim3(p.M), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((norm_kernel<T, 8>), dim3(p.M), dim3(256), 0, s, p);
 }
 
 void launch_norm(const NormParams& p, int dtype, hipStream_t s) {
   if (dtype == kF16)
-    hipLaunchKernelGGL(norm_kernel<_Float16>, dim3(p.M), dim3(256), 0, s, p);
+    launch_norm_t<_Float16>(p, s);
   else
-    hipLaunchKernelGGL(norm_kernel<__bf16>, dim3(p.M), dim3(256), 0, s, p);
+    launch_norm_t<__bf16>(p, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -58,6 +58,7 @@ int validate_model(const tv_llama_model* m, const char* who) {
     return fail(TV_EINVAL, "%s: bad model shape", who);
   if (m->dim % 32 || (m->n_heads * m->head_dim) % 32 || m->hidden_dim % 32)
     return fail(TV_EUNSUPPORTED, "%s: dim, n_heads*head_dim and hidden_dim must be multiples of 32", who);
+  if (m->dim > 8192) return fail(TV_EUNSUPPORTED, "%s: dim %d above 8192", who, m->dim);
   if (m->head_dim % 2 || m->vocab_size % 4)
     return fail(TV_EUNSUPPORTED, "%s: head_dim must be even and vocab_size a multiple of 4", who);
   if (!m->tok_embeddings || !m->wqkv || !m->wo || !m->w13 || !m->w2 || !m->attention_norm || !m->ffn_norm ||
@@ -326,7 +327,7 @@ int tv_linear(void* out, const void* a, const void* w, int M, int N, int K, int6
     return fail(TV_EINVAL, "tv_linear: logits output needs ldo >= N, ldo %% 4 == 0, 16-byte alignment");
   if (epilogue == TV_EPI_PARTIAL && !aligned16(out)) return fail(TV_EINVAL, "tv_linear: partials must be 16-byte aligned");
   const long long splits = splits_of(K, k_split);
-  if ((N + tv::kLinBN - 1) / tv::kLinBN > 0x7fffffff || splits > 65535 || (M + tv::kLinBM - 1) / tv::kLinBM > 65535)
+  if ((N + tv::kLinBN - 1) / tv::kLinBN > 65535 || (M + tv::kLinBM - 1) / tv::kLinBM > 65535)
     return fail(TV_EINVAL, "tv_linear: grid too large");
   linear(a, w, M, N, K, lda, k_split, epilogue, out, ldo, reinterpret_cast<unsigned long long*>(keys), dtype,
          reinterpret_cast<hipStream_t>(stream));
@@ -339,6 +340,7 @@ int tv_rms_norm_residual(float* x, void* xh, const float* part, int splits, cons
   if (!mfma_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_rms_norm_residual: dtype %d (float16 / bfloat16 only)", dtype);
   if (M <= 0 || dim <= 0 || dim % 4 || (part && splits <= 0) || (emb && vocab <= 0))
     return fail(TV_EINVAL, "tv_rms_norm_residual: bad shape (M=%d, dim=%d, splits=%d)", M, dim, splits);
+  if (dim > 8192) return fail(TV_EUNSUPPORTED, "tv_rms_norm_residual: dim %d above 8192", dim);
   if (!aligned16(x) || !aligned16(weight) || (part && !aligned16(part)) || (uintptr_t)xh % 8 ||
       (emb && (uintptr_t)emb % 8))
     return fail(TV_EINVAL, "tv_rms_norm_residual: misaligned buffer");

@@ -22,7 +22,7 @@
 
 namespace tv {
 
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, int PF>
 __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams p) {
   constexpr int KS = D / 32;        // MFMA k steps over the head dim
   constexpr int DB = D / 16;        // 16-dim blocks of O^T
@@ -32,7 +32,7 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   constexpr int SO = NW * 16 * D * 2;   // merge buffer [NW][16][D] floats, in elements
   constexpr int UNION = SVT > SO ? SVT : SO;
   __shared__ __attribute__((aligned(16))) uint16_t smem[16 * D + UNION];
-  __shared__ uint32_t snew[D];      // k (D/2 words) then v, for the write after attention
+  __shared__ __attribute__((aligned(16))) uint32_t snew[D];   // k (D/2 words) then v of the new token
   __shared__ float sm[NW][16];
   __shared__ float sl[NW][16];
   uint16_t* sq = smem;                       // [16 heads][D] query rows, heads >= G zero
@@ -53,16 +53,27 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   const int len = ctx <= 0 ? width : min(ctx, width);
   const int* bt = p.block_tables + (size_t)b * p.bt_stride;
   const int pos = p.positions[b];
+  const size_t rs = (size_t)p.Hkv * D;   // elements between cache rows
+  T* kcache = reinterpret_cast<T*>(p.k_cache) + (size_t)kvh * D;
+  T* vcache = reinterpret_cast<T*>(p.v_cache) + (size_t)kvh * D;
+  const int ntiles = (len + 31) >> 5;
+  const int nt = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;   // this wave's tiles: wave + NW j
+
+  // Block ids of this wave's tiles j0 .. j0+31, one per lane: lane 2 i + h holds
+  // the block of half h (16 tokens) of tile j0 + i.  One vector load instead of
+  // a dependent table lookup per tile.
+  auto load_blocks = [&](int j0) {
+    const int tok = (wave + NW * (j0 + (lane >> 1))) * 32 + 16 * (lane & 1);
+    return bt[min(tok / bs, p.max_blocks - 1)];
+  };
+  int blkv = load_blocks(0);
+
+  // ---- q, k, v of the new token -----------------------------------------
   long long slot = -1;
   if (pos >= 0 && pos / bs < p.bt_stride) {
     const int blk = bt[pos / bs];
     if (blk >= 0 && blk < p.num_blocks) slot = (long long)blk * bs + pos % bs;
   }
-  const size_t rs = (size_t)p.Hkv * D;   // elements between cache rows
-  T* kcache = reinterpret_cast<T*>(p.k_cache) + (size_t)kvh * D;
-  T* vcache = reinterpret_cast<T*>(p.v_cache) + (size_t)kvh * D;
-
-  // ---- q, k, v of the new token -----------------------------------------
   {
     const int nq = G * (D / 2);
     const int pr = min(max(pos, 0), p.rope_len - 1);
@@ -96,17 +107,17 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
       const uint32_t w = pack2<T>(v0, v1);
       if (it < nq) {
         *reinterpret_cast<uint32_t*>(&sq[(it / (D / 2)) * D + 2 * d2]) = w;
-      } else if (p.write_before) {
-        if (slot >= 0)
-          *reinterpret_cast<uint32_t*>((it < nq + D / 2 ? kcache : vcache) + (size_t)slot * rs + 2 * d2) = w;
       } else {
         snew[it - nq] = w;
+        // written now for later steps; this step's attention takes them from snew
+        if (p.write_before && slot >= 0)
+          *reinterpret_cast<uint32_t*>((it < nq + D / 2 ? kcache : vcache) + (size_t)slot * rs + 2 * d2) = w;
       }
     }
     for (int it = tid; it < (16 - G) * (D / 2); it += 64 * NW)
       *reinterpret_cast<uint32_t*>(&sq[G * D + 2 * it]) = 0u;
   }
-  __syncthreads();   // q rows in LDS; the slot written before any wave reads it
+  lds_barrier();   // q rows and the new k/v in LDS
 
   // ---- attention over [0, len) ----------------------------------------------
   u32x4 qf[KS];
@@ -119,8 +130,6 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
   uint16_t* vt = svt + wave * (D * VP);
-  const int ntiles = (len + 31) >> 5;
-  const int nt = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;   // this wave's tiles: wave + NW j
 
   struct Tile {
     u32x4 k[2][KS];
@@ -130,11 +139,12 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   };
   // Tile j of this wave: tokens t0 .. t0+31, two 16-token halves each inside
   // one cache block (block_size is a multiple of 16).
-  auto load = [&](int j, Tile& r) {
+  // (j - j0 < 32: the block ids of tiles j0 .. j0+31 are in blkv)
+  auto load = [&](int j, int j0, Tile& r) {
     const int t0 = (wave + NW * j) * 32;
     r.t0 = t0;
-    int b0 = bt[min(t0 / bs, p.max_blocks - 1)];
-    int b1 = bt[min((t0 + 16) / bs, p.max_blocks - 1)];
+    int b0 = __builtin_amdgcn_readlane(blkv, 2 * (j - j0));
+    int b1 = __builtin_amdgcn_readlane(blkv, 2 * (j - j0) + 1);
     r.ok0 = (unsigned)b0 < (unsigned)p.num_blocks;
     r.ok1 = (unsigned)b1 < (unsigned)p.num_blocks;
     b0 = r.ok0 ? b0 : 0;
@@ -159,7 +169,24 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
     }
   };
 
-  auto consume = [&](const Tile& r) {
+  auto consume = [&](Tile& r) {
+    if (p.write_before && r.t0 <= pos && pos < r.t0 + 32) {
+      // the new token's row, from LDS (its cache store need not be visible yet)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+        if (r.t0 + 16 * tb + col == pos) {
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) r.k[tb][ks] = *reinterpret_cast<const u32x4*>(&snew[16 * ks + 4 * g]);
+        }
+#pragma unroll
+      for (int i = 0; i < VU; ++i) {
+        const int unit = lane + 64 * i;
+        const int tok = r.t0 + 2 * (unit & 15);
+        const u32x4 nv = *reinterpret_cast<const u32x4*>(&snew[D / 2 + 4 * (unit >> 4)]);
+        if (tok == pos) r.v[i][0] = nv;
+        if (tok + 1 == pos) r.v[i][1] = nv;
+      }
+    }
     // S^T: st[tb][i] = q_head(col) . k(token t0 + 16 tb + 4 g + i)
     f32x4 st[2];
 #pragma unroll
@@ -237,25 +264,31 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
     }
   };
 
-  if (nt > 0) {
-    // two tiles in flight; the loads are unconditional (the last tile is
-    // re-read) so the compiler waits for exactly the tile it consumes
-    Tile ta, tb;
-    load(0, ta);
-    load(min(1, nt - 1), tb);
-    int j = 0;
-    for (; j + 1 < nt; j += 2) {
-      consume(ta);
-      load(min(j + 2, nt - 1), ta);
-      consume(tb);
-      load(min(j + 3, nt - 1), tb);
+  // Chunks of 32 tiles (one block id per lane and half); within a chunk PF
+  // tiles are in flight and the loads are unconditional (the chunk's last tile
+  // is re-read) so the compiler waits for exactly the tile it consumes.
+  for (int j0 = 0; j0 < nt; j0 += 32) {
+    if (j0 > 0) blkv = load_blocks(j0);
+    const int je = min(nt, j0 + 32);
+    Tile t[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) load(min(j0 + i, je - 1), j0, t[i]);
+    int j = j0;
+    for (; j + PF - 1 < je; j += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        consume(t[i]);
+        load(min(j + PF + i, je - 1), j0, t[i]);
+      }
     }
-    if (j < nt) consume(ta);
+#pragma unroll
+    for (int i = 0; i < PF - 1; ++i)
+      if (j + i < je) consume(t[i]);
   }
 
   // ---- merge the waves ----------------------------------------------------------
   lsum = sum_over_g(lsum);
-  __syncthreads();   // every wave is done with its V^T tile: the buffer becomes [NW][16][D] floats
+  lds_barrier();   // every wave is done with its V^T tile: the buffer becomes [NW][16][D] floats
   float* so = reinterpret_cast<float*>(svt);
   if (g == 0) {
     sm[wave][col] = m;
@@ -264,7 +297,7 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
 #pragma unroll
   for (int db = 0; db < DB; ++db)
     *reinterpret_cast<f32x4*>(&so[(wave * 16 + col) * D + db * 16 + 4 * g]) = o[db];
-  __syncthreads();
+  lds_barrier();
   T* out = reinterpret_cast<T*>(p.out) + ((size_t)b * p.Hq + (size_t)kvh * G) * D;
   for (int it = tid; it < G * D; it += 64 * NW) {
     const int h = it / D;
@@ -292,17 +325,25 @@ bool step_attn_supported(int head_dim, int group, int block_size) {
   return (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 16 && block_size % 16 == 0;
 }
 
-// Waves per work-group: 8 at head_dim 64 (two per SIMD with one work-group per
-// CU at batch 64 x 4 KV heads); 4 at head_dim 128, whose double-buffered tiles
-// need more than the 256 registers two waves per SIMD allow.
+#ifndef TV_STEP_ATTN_W64
+#define TV_STEP_ATTN_W64 8    // waves per work-group at head_dim 64
+#endif
+#ifndef TV_STEP_ATTN_PF64
+#define TV_STEP_ATTN_PF64 2   // tiles in flight per wave at head_dim 64
+#endif
+
+// head_dim 64: 8 waves (two per SIMD with one work-group per CU at batch 64 x 4
+// KV heads) and two tiles in flight per wave; head_dim 128: 4 waves, whose
+// larger tiles need more than the 256 registers two waves per SIMD allow.
 void launch_step_attn(const StepAttnParams& p, int head_dim, int dtype, hipStream_t s) {
+  constexpr int W64 = TV_STEP_ATTN_W64, PF64 = TV_STEP_ATTN_PF64;
   const dim3 grid(p.Hkv, p.B);
   if (dtype == kF16) {
-    if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<_Float16, 64, 8>), grid, dim3(512), 0, s, p);
-    else hipLaunchKernelGGL((step_attn_kernel<_Float16, 128, 4>), grid, dim3(256), 0, s, p);
+    if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<_Float16, 64, W64, PF64>), grid, dim3(64 * W64), 0, s, p);
+    else hipLaunchKernelGGL((step_attn_kernel<_Float16, 128, 4, 2>), grid, dim3(256), 0, s, p);
   } else {
-    if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<__bf16, 64, 8>), grid, dim3(512), 0, s, p);
-    else hipLaunchKernelGGL((step_attn_kernel<__bf16, 128, 4>), grid, dim3(256), 0, s, p);
+    if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<__bf16, 64, W64, PF64>), grid, dim3(64 * W64), 0, s, p);
+    else hipLaunchKernelGGL((step_attn_kernel<__bf16, 128, 4, 2>), grid, dim3(256), 0, s, p);
   }
 }
 
