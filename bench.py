@@ -217,6 +217,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--primary-only", action="store_true")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="run only the end-to-end TinyLlama decode and print its result (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -228,6 +230,9 @@ def main():
     from tinyvllm_amd import workloads
 
     torch.cuda.set_device(0)
+    if args.e2e_only:
+        print(json.dumps(bench_e2e()), flush=True)
+        return
     log("bench: config3 decode (B256 Hq32 Hkv8 D128 fp16)")
     wl3 = workloads.config3_decode_llama3_8b()
     torch.cuda.synchronize()
