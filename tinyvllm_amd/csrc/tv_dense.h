@@ -12,7 +12,7 @@ constexpr int kLinBM = 64;    // rows of A (tokens) per work-group
 constexpr int kLinBN = 64;    // rows of W (output features) per work-group, 16 per wave
 constexpr int kLinKC = 256;   // K elements staged in LDS per chunk
 
-// Y = A W^T over the K range of one split; grid (ceil(N/64), splits, ceil(M/64)).
+// Y = A W^T over the K range of one split; grid (splits, ceil(N/64), ceil(M/64)).
 struct LinearParams {
   const void* a;          // [M, K] at row stride lda
   const void* w;          // [N, K] dense
