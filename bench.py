@@ -219,6 +219,8 @@ def main():
     ap.add_argument("--primary-only", action="store_true")
     ap.add_argument("--e2e-only", action="store_true",
                     help="run only the end-to-end TinyLlama decode and print its result (profiling)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the causal prefill + K/V write workload and print its result (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -232,6 +234,9 @@ def main():
     torch.cuda.set_device(0)
     if args.e2e_only:
         print(json.dumps(bench_e2e()), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps(bench_prefill(args.steps, args.warmup)), flush=True)
         return
     log("bench: config3 decode (B256 Hq32 Hkv8 D128 fp16)")
     wl3 = workloads.config3_decode_llama3_8b()

@@ -49,8 +49,10 @@ const char* tv_last_error(void);
 /*
  * Workspace (bytes) needed by tv_paged_decode for the split-context partials:
  * num_seqs * num_heads * ceil(max_blocks*block_size / partition_size)
- * * (head_dim + 2) floats, or 0 when every sequence fits one partition.
- * Host-only computation.
+ * * (head_dim + 2) floats.  When every sequence fits one partition and
+ * num_seqs >= 32 it is num_seqs ints (rounded up to 256 bytes) for a
+ * longest-first schedule of the sequences, which tv_paged_decode uses when
+ * the caller provides it and skips otherwise; else 0.  Host-only computation.
  */
 size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
                                        int max_blocks, int block_size, int partition_size);
@@ -70,7 +72,8 @@ size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim
  * for that sequence.
  * partition_size: tokens per work-group (multiple of 16, > 0).  Sequences longer
  * than one partition are split (flash-decoding) and merged by a second kernel;
- * that needs `workspace` of tv_paged_decode_workspace_bytes(...) bytes.
+ * that needs `workspace` of tv_paged_decode_workspace_bytes(...) bytes (for an
+ * unsplit launch the workspace is optional and only holds the schedule).
  * q, caches and out share `dtype`; out may instead be TV_F32 (out_dtype).
  */
 int tv_paged_decode(void* out, const void* queries, const void* k_cache, const void* v_cache,

@@ -153,6 +153,22 @@ def test_invalid_block_id_gives_nan_not_fault():
     assert np.abs(out[:1] - want).max() <= 1e-4
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_large_batch_runs_longest_first(dtype):
+    """48 sequences of mixed lengths in one partition: the launch is scheduled
+    longest first through the workspace; results stay per sequence, including
+    ties, a context of 0 (whole padded width) and contexts beyond the table."""
+    rng = np.random.Generator(np.random.PCG64(11))
+    ctx = rng.integers(1, 200, 48).astype(np.int32)
+    ctx[[3, 17, 30]] = 150           # ties
+    ctx[5] = 0                        # reference all-masked mean of the padded gather
+    case = build_case(12, ctx.tolist(), 16, 4, 128, 16, dtype, width=13)
+    q, kc, vc, bt, cl = case
+    cl = cl.copy()
+    cl[9] = 100000                    # beyond the table: truncated to its width
+    check((q, kc, vc, bt, cl), 16, 4, 128, 16, dtype, partition_size=4096)
+
+
 def test_deterministic():
     case = build_case(11, [100, 700, 3], 32, 8, 128, 16, torch.float16)
     a = run(*case, 32, 8, 128, 16, partition_size=128)

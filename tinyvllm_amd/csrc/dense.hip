@@ -31,15 +31,6 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
   return ((unsigned long long)u << 32) | (0xFFFFFFFFu - (uint32_t)n);
 }
 
-// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit dwords, no swizzle).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned long long bytes) {
-  const unsigned n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (unsigned)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
-}
-__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 #ifndef TV_LINEAR_MIN_BLOCKS

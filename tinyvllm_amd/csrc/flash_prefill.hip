@@ -378,6 +378,344 @@ __global__ void __launch_bounds__(256 * KSPLIT) prefill_mfma_kernel(const Prefil
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA kernel, head_dim 64: register-lean softmax, double-buffered tiles
+// ---------------------------------------------------------------------------
+//
+// A work-group owns 64 query rows of one head.  KS groups of QW = 4 / RB waves
+// split the row block's key tiles (group s takes tiles kt0 + s + KS j); every
+// wave owns RB blocks of 16 query rows, so each K / V fragment read from LDS
+// feeds RB matrix products.  Per 64-key tile a wave computes S^T = K Q^T with
+// Q pre-scaled by scale * log2(e) and the accumulator initialised to -m (the
+// running reference maximum of the query), so the scores come out of the
+// matrix cores already in the log2 domain relative to m and go straight into
+// v_exp_f32.  m is raised only when a tile exceeds it by more than 8, which
+// after the first tile is rare.  V is staged row-major in LDS and read as
+// the V^T operand with ds_read_b64_tr_b16; the softmax row sums come from one
+// extra MFMA of P against a register of ones.  Tiles are double-buffered in LDS
+// and loaded two steps ahead through buffer loads whose range ends at the last
+// key row (rows past kv_len read as zero), one barrier per step.
+
+// ds_read_b64_tr_b16: within each 16-lane row of the wave, lane i receives
+// element i % 4 of the 64-bit words addressed by lanes 4 k + i / 4, k = 0..3.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* ptr) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(ptr)));
+}
+
+template <typename T> __device__ __forceinline__ u32x4 scale8(u32x4 w, float c) {
+  u32x4 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float a, b;
+    unpack2<T>(w[k], a, b);
+    r[k] = pack2<T>(a * c, b * c);
+  }
+  return r;
+}
+
+template <typename T> constexpr uint32_t kOnes2 = 0;
+template <> constexpr uint32_t kOnes2<_Float16> = 0x3C003C00u;
+template <> constexpr uint32_t kOnes2<__bf16> = 0x3F803F80u;
+
+__device__ __forceinline__ float max16(const f32x4 (&st)[4]) {
+  const float a = fmaxf(fmaxf(st[0][0], st[0][1]), st[0][2]);
+  const float b = fmaxf(fmaxf(st[0][3], st[1][0]), st[1][1]);
+  const float c = fmaxf(fmaxf(st[1][2], st[1][3]), st[2][0]);
+  const float d = fmaxf(fmaxf(st[2][1], st[2][2]), st[2][3]);
+  const float e = fmaxf(fmaxf(st[3][0], st[3][1]), st[3][2]);
+  return fmaxf(fmaxf(fmaxf(a, b), fmaxf(c, d)), fmaxf(e, st[3][3]));
+}
+
+#ifndef TV_PREFILL_RB
+#define TV_PREFILL_RB 2       // 16-row query blocks per wave (head_dim 64)
+#endif
+#ifndef TV_PREFILL_KS
+#define TV_PREFILL_KS 2       // key-tile groups per work-group (head_dim 64)
+#endif
+#ifndef TV_PREFILL_WAVES_PER_EU
+#define TV_PREFILL_WAVES_PER_EU 2
+#endif
+
+template <typename T, int D, int RB, int KS>
+__global__ void __launch_bounds__(256 / RB * KS) __attribute__((amdgpu_waves_per_eu(TV_PREFILL_WAVES_PER_EU)))
+prefill_fa_kernel(const PrefillParams p) {
+  constexpr int QW = 4 / RB;              // waves of a group along the 64 query rows
+  constexpr int GT = 64 * QW;             // threads of a group
+  constexpr int BM = kPrefillBM;
+  constexpr int BN = 64;                  // keys per tile
+  constexpr int KP = D + 8;               // K tile pitch (elements): 16-byte reads of 16 rows hit distinct banks
+  constexpr int VP = D + 16;              // V tile pitch: the transposing reads of 16 rows x 32 B use every bank twice
+  constexpr int SKT = BN * KP;
+  constexpr int BUF = SKT + BN * VP;      // one K + V tile buffer (elements)
+  constexpr int KSD = D / 32;             // MFMA steps over the head dim
+  constexpr int DB = D / 16;              // 16-dim blocks of O^T
+  constexpr int CPR = D / 8;              // 16-byte vectors per row
+  constexpr int NV = BN * CPR / GT;       // vectors per thread per tile, each of K and V
+  constexpr int MERGE = KS > 1 ? KS * BM * (D + 2) * 2 : 0;   // merge area (uint16 units)
+  constexpr int SMEM = KS * 2 * BUF > MERGE ? KS * 2 * BUF : MERGE;
+  static_assert(kPrefillBN == BN && NV * GT == BN * CPR, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
+
+  const int grp = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
+  const int tid = threadIdx.x - grp * GT;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  uint16_t* const tiles = smem + grp * 2 * BUF;
+
+  const int h = prefill_head(blockIdx.x, p.num_heads, p.xcd_remap);
+  int qt, chunk, nchunks;
+  prefill_unit(p, blockIdx.y, qt, chunk, nchunks);
+  const int kvh = h / (p.num_heads / p.num_kv_heads);
+  const int nkt = prefill_key_tiles(p, qt);
+  const int kt0 = chunk * p.chunk_tiles;
+  const int kt1 = min(kt0 + p.chunk_tiles, nkt);
+  const float c = p.scale * kLog2e;
+  const int row0 = qt * BM + wave * RB * 16;   // first query row of this wave
+
+  int qi[RB];
+  u32x4 qf[RB][KSD];
+  {
+    const T* qg = reinterpret_cast<const T*>(p.q) + (size_t)h * D;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      qi[r] = row0 + r * 16 + col;
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks)
+        qf[r][ks] = qi[r] < p.q_len
+                        ? scale8<T>(*reinterpret_cast<const u32x4*>(qg + (size_t)qi[r] * p.q_stride + ks * 32 + g * 8), c)
+                        : u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // global -> LDS staging: thread vector i = (row, 16-byte column chunk)
+  const T* kbase = reinterpret_cast<const T*>(p.k) + (size_t)kvh * D;
+  const T* vbase = reinterpret_cast<const T*>(p.v) + (size_t)kvh * D;
+  int koff[NV], voff[NV], kdst[NV], vdst[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = tid + i * GT;
+    const int row = v / CPR, ch = v - (v / CPR) * CPR;
+    koff[i] = (int)(row * p.k_stride + ch * 8) * (int)sizeof(T);
+    voff[i] = (int)(row * p.v_stride + ch * 8) * (int)sizeof(T);
+    kdst[i] = row * KP + ch * 8;
+    vdst[i] = SKT + row * VP + ch * 8;
+  }
+  struct Stage {
+    u32x4 k[NV], v[NV];
+  };
+  auto tile_of = [&](int j) { return min(kt0 + grp + KS * j, kt1 - 1); };
+  auto gload = [&](int j, Stage& s) {
+    const int k0 = tile_of(j) * BN;
+    const long long rows = p.kv_len - k0;   // >= 1
+    const __amdgpu_buffer_rsrc_t rk =
+        make_rsrc(kbase + (size_t)k0 * p.k_stride, (unsigned long long)((rows - 1) * p.k_stride + D) * sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv =
+        make_rsrc(vbase + (size_t)k0 * p.v_stride, (unsigned long long)((rows - 1) * p.v_stride + D) * sizeof(T));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) s.k[i] = buffer_load16(rk, koff[i], 0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) s.v[i] = buffer_load16(rv, voff[i], 0);
+  };
+  auto lstore = [&](const Stage& s, int b) {
+    uint16_t* t = tiles + b * BUF;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) *reinterpret_cast<u32x4*>(t + kdst[i]) = s.k[i];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) *reinterpret_cast<u32x4*>(t + vdst[i]) = s.v[i];
+  };
+
+  f32x4 oacc[RB][DB + 1];
+  f32x4 negm[RB];       // -m in every element: the S^T accumulator's initial value
+  float mref[RB];       // running reference maximum (log2 units) of this lane's query
+  float thr[RB];        // rescale threshold: -FLT_MAX until the first visible key
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+#pragma unroll
+    for (int db = 0; db <= DB; ++db) oacc[r][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    negm[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mref[r] = 0.0f;
+    thr[r] = -__FLT_MAX__;
+  }
+  const u32x4 ones = u32x4{kOnes2<T>, kOnes2<T>, kOnes2<T>, kOnes2<T>};
+
+  auto compute = [&](int b, int kt) {
+    const uint16_t* sk = tiles + b * BUF;
+    const uint16_t* sv = sk + SKT;
+    const int k0 = kt * BN;
+    u32x4 kf[4][KSD];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks)
+        kf[kb][ks] = *reinterpret_cast<const u32x4*>(sk + (kb * 16 + col) * KP + ks * 32 + g * 8);
+    f32x4 st[RB][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        st[r][kb] = mfma16x16x32<T>(kf[kb][0], qf[r][0], negm[r]);
+#pragma unroll
+        for (int ks = 1; ks < KSD; ++ks) st[r][kb] = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], st[r][kb]);
+      }
+    // V^T fragments: rows (keys) ks2*32 + 4g + (col >> 2) (+16), columns db*16 + 4 (col & 3)
+    u32x4 vf[DB][2];
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const uint16_t* a = sv + (ks2 * 32 + 4 * g + (col >> 2)) * VP + db * 16 + 4 * (col & 3);
+        const u32x2 lo = lds_read_tr16(a);
+        const u32x2 hi = lds_read_tr16(a + 16 * VP);
+        vf[db][ks2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+    if (!(k0 + BN <= p.kv_len && (!p.causal || k0 + BN - 1 <= row0))) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int lim = p.causal ? min(p.kv_len - 1, qi[r]) : p.kv_len - 1;   // last visible key
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            st[r][kb][i] = k0 + kb * 16 + 4 * g + i <= lim ? st[r][kb][i] : kNegInf;
+      }
+    }
+    float mt[RB];
+    bool need_any = false;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      mt[r] = max_over_g(max16(st[r]));
+      need_any = need_any || mt[r] > thr[r];
+    }
+    if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const bool need = mt[r] > thr[r];
+        const float delta = need ? mt[r] : 0.0f;
+        const float alpha = need && thr[r] > 0.0f ? fast_exp2(-delta) : 1.0f;
+#pragma unroll
+        for (int db = 0; db <= DB; ++db) oacc[r][db] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) st[r][kb] -= delta;
+        mref[r] += delta;
+        negm[r] = f32x4{-mref[r], -mref[r], -mref[r], -mref[r]};
+        thr[r] = need ? 8.0f : thr[r];
+      }
+    }
+    u32x4 pf[RB][2];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        // reduction index 8g + j: key 4g + j of block 2 ks2 (j < 4), 4g + j - 4 of block 2 ks2 + 1
+        pf[r][kb >> 1][(kb & 1) * 2] = pack2<T>(fast_exp2(st[r][kb][0]), fast_exp2(st[r][kb][1]));
+        pf[r][kb >> 1][(kb & 1) * 2 + 1] = pack2<T>(fast_exp2(st[r][kb][2]), fast_exp2(st[r][kb][3]));
+      }
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[r][db] = mfma16x16x32<T>(vf[db][ks2], pf[r][ks2], oacc[r][db]);
+        oacc[r][DB] = mfma16x16x32<T>(ones, pf[r][ks2], oacc[r][DB]);
+      }
+  };
+
+  // group tile sequence kt0 + grp + KS j; steps padded to even so the loop body
+  // (two steps, one per LDS buffer) has no exit and the same loads on every path
+  const int nsteps = (kt1 - kt0 + KS - 1) / KS;
+  const int nsteps2 = (nsteps + 1) & ~1;
+  Stage sa, sb;
+  gload(0, sa);
+  gload(1, sb);
+  lstore(sa, 0);
+  gload(2, sa);
+  lds_barrier();
+  for (int j = 0; j < nsteps2; j += 2) {
+    if (kt0 + grp + KS * j < kt1) compute(0, kt0 + grp + KS * j);
+    lstore(sb, 1);
+    gload(j + 3, sb);
+    lds_barrier();
+    if (kt0 + grp + KS * (j + 1) < kt1) compute(1, kt0 + grp + KS * (j + 1));
+    lstore(sa, 0);
+    gload(j + 4, sa);
+    lds_barrier();
+  }
+
+  float mfin[RB], lfin[RB];
+  if constexpr (KS > 1) {
+    float* so = reinterpret_cast<float*>(smem);   // [KS][64 rows][D]
+    float* ssum = so + KS * BM * D;               // [KS][64 rows]
+    float* smax = ssum + KS * BM;                 // [KS][64 rows]
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int row = (wave * RB + r) * 16 + col;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(&so[(grp * BM + row) * D + db * 16 + 4 * g]) = oacc[r][db];
+      if (g == 0) {
+        ssum[grp * BM + row] = oacc[r][DB][0];
+        smax[grp * BM + row] = thr[r] > 0.0f ? mref[r] : kNegInf;
+      }
+    }
+    lds_barrier();
+    if (grp != 0) return;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int row = (wave * RB + r) * 16 + col;
+      float M = kNegInf;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) M = fmaxf(M, smax[s * BM + row]);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[r][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float L = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const float ms = smax[s * BM + row];
+        const float f = ms == kNegInf ? 0.0f : fast_exp2(ms - M);
+        L = fmaf(ssum[s * BM + row], f, L);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          oacc[r][db] += *reinterpret_cast<const f32x4*>(&so[(s * BM + row) * D + db * 16 + 4 * g]) * f;
+      }
+      mfin[r] = M;
+      lfin[r] = L;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      mfin[r] = thr[r] > 0.0f ? mref[r] : kNegInf;
+      lfin[r] = oacc[r][DB][0];
+    }
+  }
+
+  const int nqt = (p.q_len + BM - 1) / BM;
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    if (qi[r] >= p.q_len) continue;
+    const float inv = 1.0f / lfin[r];
+    if (nchunks == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        store4<T>(p.out, (size_t)qi[r] * p.out_stride + (size_t)h * D + db * 16 + 4 * g, oacc[r][db] * inv,
+                  p.out_dtype);
+    } else {
+      const size_t unit = ((size_t)h * nqt + qt) * p.max_chunks + chunk;
+      const int row = qi[r] - qt * BM;
+      float* po = p.part_o + (unit * BM + row) * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(po + db * 16 + 4 * g) = oacc[r][db] * inv;
+      if (g == 0) {
+        p.part_ml[(unit * BM + row) * 2] = mfin[r];
+        p.part_ml[(unit * BM + row) * 2 + 1] = lfin[r];
+      }
+    }
+  }
+}
+
 // Merge the key-chunk partials of query tiles that were split.  grid (Hq, nqt).
 template <int D>
 __global__ void __launch_bounds__(256) prefill_merge_kernel(const PrefillParams p) {
@@ -493,8 +831,10 @@ bool prefill_uses_mfma(const PrefillParams& p, int dtype) {
   // 16-byte fragment loads: token strides and base addresses must be 16 B aligned.
   const bool aligned = p.q_stride % 8 == 0 && p.k_stride % 8 == 0 && p.v_stride % 8 == 0 &&
                        ((uintptr_t)p.q % 16) == 0 && ((uintptr_t)p.k % 16) == 0 && ((uintptr_t)p.v % 16) == 0;
+  // 32-bit buffer offsets inside one 64-row key tile
+  const bool small_stride = p.k_stride < (1ll << 24) && p.v_stride < (1ll << 24);
   return (dtype == kF16 || dtype == kBF16) && p.head_dim == p.head_dim_v &&
-         (p.head_dim == 64 || p.head_dim == 128) && aligned;
+         (p.head_dim == 64 || p.head_dim == 128) && aligned && small_stride;
 }
 
 size_t prefill_workspace_bytes(const PrefillParams& p, int dtype) {
@@ -524,6 +864,7 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     }
     const bool d64 = pp.head_dim == 64;
     const dim3 grid(pp.num_heads, units);
+#ifdef TV_PREFILL_V1
     constexpr int KSP = TV_PREFILL_KSPLIT;
     const dim3 block(256 * KSP);
     if (dtype == kF16) {
@@ -533,6 +874,17 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
       if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 64, KSP>), grid, block, 0, stream, pp);
       else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
     }
+#else
+    constexpr int RB = TV_PREFILL_RB, KS = TV_PREFILL_KS;
+    const dim3 block(256 / RB * KS);
+    if (dtype == kF16) {
+      if (d64) hipLaunchKernelGGL((prefill_fa_kernel<_Float16, 64, RB, KS>), grid, block, 0, stream, pp);
+      else hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128, 1>), grid, dim3(256), 0, stream, pp);
+    } else {
+      if (d64) hipLaunchKernelGGL((prefill_fa_kernel<__bf16, 64, RB, KS>), grid, block, 0, stream, pp);
+      else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
+    }
+#endif
     if (max_chunks > 1) {
       const dim3 mgrid(pp.num_heads, (pp.q_len + kPrefillBM - 1) / kPrefillBM);
       if (d64) hipLaunchKernelGGL((prefill_merge_kernel<64>), mgrid, dim3(256), 0, stream, pp);

@@ -74,6 +74,7 @@ struct DecodeParams {
   int partition_size;        // tokens per work-group
   int max_parts;             // ceil(max_blocks*block_size / partition_size)
   int out_dtype;
+  const int* order;          // [B] sequence of work-group row z (longest first), or null: z
 };
 
 __device__ __forceinline__ int decode_len(const DecodeParams& p, int b, float& bias) {
@@ -166,7 +167,7 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
   const int r = lane / LPR;
   const int c = lane % LPR;
   const int part = blockIdx.x;
-  const int b = blockIdx.z;
+  const int b = p.order ? p.order[blockIdx.z] : (int)blockIdx.z;
   const int kh = blockIdx.y / p.head_chunks;
   const int group = p.num_heads / p.num_kv_heads;
   const int h0 = kh * group + (blockIdx.y % p.head_chunks) * GT;
@@ -468,6 +469,8 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
 // grid (Hq, B) and 64 threads; sequences that fit one partition were written by
 // the main kernel and are skipped here.
 __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodeParams p, int head_dim);
+__global__ void __launch_bounds__(256) decode_order_kernel(const int* context_lens, int num_seqs, int width,
+                                                           int* order);
 
 
 }  // namespace tv

@@ -66,4 +66,30 @@ __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodePar
   }
 }
 
+// Longest-first schedule of an unsplit decode launch: order[rank] = b, where
+// rank counts the sequences that attend to more positions than b (ties by
+// index).  Work-groups are dispatched in grid order, so the longest sequences
+// start first and the last ones to start are short: the launch does not end
+// on a few long sequences streaming while most CUs idle.  Any permutation is
+// correct; this one only shortens the tail.  grid ceil(B / 256), 256 threads.
+__global__ void __launch_bounds__(256) decode_order_kernel(const int* context_lens, int num_seqs, int width,
+                                                           int* order) {
+  __shared__ int sl[256];
+  const int b = blockIdx.x * 256 + threadIdx.x;
+  auto eff = [&](int ctx) { return ctx <= 0 ? width : (ctx < width ? ctx : width); };
+  const int mine = b < num_seqs ? eff(context_lens[b]) : 0;
+  int rank = 0;
+  for (int base = 0; base < num_seqs; base += 256) {
+    __syncthreads();
+    if (base + (int)threadIdx.x < num_seqs) sl[threadIdx.x] = eff(context_lens[base + threadIdx.x]);
+    __syncthreads();
+    const int n = min(256, num_seqs - base);
+    for (int j = 0; j < n; ++j) {
+      const int lj = sl[j];
+      rank += (lj > mine) || (lj == mine && base + j < b);
+    }
+  }
+  if (b < num_seqs) order[rank] = b;
+}
+
 }  // namespace tv

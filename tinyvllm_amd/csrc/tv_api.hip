@@ -87,6 +87,10 @@ int tv_abi_version(void) { return 3; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
+// Unsplit launches of at least this many sequences run longest first
+// (decode_order_kernel), which needs num_seqs ints of workspace.
+static constexpr int kDecodeOrderMinSeqs = 32;
+
 size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_blocks,
                                        int block_size, int partition_size) {
   if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0 ||
@@ -94,7 +98,7 @@ size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim
     return 0;
   const long long width = (long long)max_blocks * block_size;
   const long long parts = (width + partition_size - 1) / partition_size;
-  if (parts <= 1) return 0;
+  if (parts <= 1) return num_seqs >= kDecodeOrderMinSeqs ? ((size_t)num_seqs * sizeof(int) + 255) & ~(size_t)255 : 0;
   return (size_t)num_seqs * num_heads * parts * (head_dim + 2) * sizeof(float);
 }
 
@@ -134,8 +138,10 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   const int max_parts = (int)((width + partition_size - 1) / partition_size);
   const size_t need = tv_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, max_blocks, block_size,
                                                       partition_size);
-  if (need > 0 && (!workspace || workspace_bytes < need))
+  if (max_parts > 1 && (!workspace || workspace_bytes < need))
     return fail(TV_EINVAL, "tv_paged_decode: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  // the longest-first schedule is optional: without room for it the launch runs in batch order
+  const bool ordered = max_parts == 1 && need > 0 && workspace && workspace_bytes >= need;
 
   tv::DecodeParams p{};
   p.out = out;
@@ -156,7 +162,7 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   p.partition_size = partition_size;
   p.max_parts = max_parts;
   p.out_dtype = out_dtype;
-  if (need > 0) {
+  if (max_parts > 1) {
     const size_t n_o = (size_t)num_seqs * num_heads * max_parts * head_dim;
     p.part_o = reinterpret_cast<float*>(workspace);
     p.part_ml = p.part_o + n_o;
@@ -165,6 +171,11 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
     return fail(TV_EINVAL, "tv_paged_decode: grid too large");
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (ordered) {
+    p.order = reinterpret_cast<int*>(workspace);
+    hipLaunchKernelGGL(tv::decode_order_kernel, dim3((num_seqs + 255) / 256), dim3(256), 0, s, context_lens,
+                       num_seqs, (int)width, reinterpret_cast<int*>(workspace));
+  }
   const dim3 grid(max_parts, num_kv_heads * p.head_chunks, num_seqs);
   bool launched = false;
   if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, grid, s);

@@ -173,6 +173,16 @@ template <int N> __device__ __forceinline__ float group_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit dwords, no
+// swizzle).  A load whose voffset lies at or past `bytes` returns zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned long long bytes) {
+  const unsigned n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (unsigned)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 // Work-group barrier that orders LDS traffic only.  __syncthreads() also fences
 // global memory, which makes every wave wait for all of its outstanding global
 // loads (vmcnt(0)) -- including loads issued ahead as prefetch.
