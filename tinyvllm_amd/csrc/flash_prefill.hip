@@ -419,13 +419,16 @@ template <typename T> constexpr uint32_t kOnes2 = 0;
 template <> constexpr uint32_t kOnes2<_Float16> = 0x3C003C00u;
 template <> constexpr uint32_t kOnes2<__bf16> = 0x3F803F80u;
 
-__device__ __forceinline__ float max16(const f32x4 (&st)[4]) {
-  const float a = fmaxf(fmaxf(st[0][0], st[0][1]), st[0][2]);
-  const float b = fmaxf(fmaxf(st[0][3], st[1][0]), st[1][1]);
-  const float c = fmaxf(fmaxf(st[1][2], st[1][3]), st[2][0]);
-  const float d = fmaxf(fmaxf(st[2][1], st[2][2]), st[2][3]);
-  const float e = fmaxf(fmaxf(st[3][0], st[3][1]), st[3][2]);
-  return fmaxf(fmaxf(fmaxf(a, b), fmaxf(c, d)), fmaxf(e, st[3][3]));
+// maximum of the 4 KB values of one S^T tile (v_max3 tree)
+template <int KB> __device__ __forceinline__ float max_tile(const f32x4 (&st)[KB]) {
+  float t[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) t[kb] = fmaxf(fmaxf(st[kb][0], st[kb][1]), fmaxf(st[kb][2], st[kb][3]));
+#pragma unroll
+  for (int w = 1; w < KB; w *= 2)
+#pragma unroll
+    for (int kb = 0; kb + w < KB; kb += 2 * w) t[kb] = fmaxf(t[kb], t[kb + w]);
+  return t[0];
 }
 
 #ifndef TV_PREFILL_RB
@@ -434,17 +437,20 @@ __device__ __forceinline__ float max16(const f32x4 (&st)[4]) {
 #ifndef TV_PREFILL_KS
 #define TV_PREFILL_KS 2       // key-tile groups per work-group (head_dim 64)
 #endif
+#ifndef TV_PREFILL_FA_BN
+#define TV_PREFILL_FA_BN 64
+#endif
 #ifndef TV_PREFILL_WAVES_PER_EU
 #define TV_PREFILL_WAVES_PER_EU 2
 #endif
 
-template <typename T, int D, int RB, int KS>
+template <typename T, int D, int RB, int KS, int BN>
 __global__ void __launch_bounds__(256 / RB * KS) __attribute__((amdgpu_waves_per_eu(TV_PREFILL_WAVES_PER_EU)))
 prefill_fa_kernel(const PrefillParams p) {
   constexpr int QW = 4 / RB;              // waves of a group along the 64 query rows
   constexpr int GT = 64 * QW;             // threads of a group
   constexpr int BM = kPrefillBM;
-  constexpr int BN = 64;                  // keys per tile
+  constexpr int KB = BN / 16;             // 16-key blocks of a tile
   constexpr int KP = D + 8;               // K tile pitch (elements): 16-byte reads of 16 rows hit distinct banks
   constexpr int VP = D + 16;              // V tile pitch: the transposing reads of 16 rows x 32 B use every bank twice
   constexpr int SKT = BN * KP;
@@ -453,9 +459,10 @@ prefill_fa_kernel(const PrefillParams p) {
   constexpr int DB = D / 16;              // 16-dim blocks of O^T
   constexpr int CPR = D / 8;              // 16-byte vectors per row
   constexpr int NV = BN * CPR / GT;       // vectors per thread per tile, each of K and V
-  constexpr int MERGE = KS > 1 ? KS * BM * (D + 2) * 2 : 0;   // merge area (uint16 units)
+  constexpr int MP = D + 4;               // merge row pitch (floats): the 16 rows of a store hit distinct banks
+  constexpr int MERGE = KS > 1 ? KS * BM * (MP + 2) * 2 : 0;   // merge area (uint16 units)
   constexpr int SMEM = KS * 2 * BUF > MERGE ? KS * 2 * BUF : MERGE;
-  static_assert(kPrefillBN == BN && NV * GT == BN * CPR, "tile shape");
+  static_assert(BN % 32 == 0 && NV * GT == BN * CPR, "tile shape");
   __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
 
   const int grp = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
@@ -470,9 +477,14 @@ prefill_fa_kernel(const PrefillParams p) {
   int qt, chunk, nchunks;
   prefill_unit(p, blockIdx.y, qt, chunk, nchunks);
   const int kvh = h / (p.num_heads / p.num_kv_heads);
+  // keys [kbeg, kend) of this unit (64-key units of the chunking), in BN-key tiles
   const int nkt = prefill_key_tiles(p, qt);
   const int kt0 = chunk * p.chunk_tiles;
   const int kt1 = min(kt0 + p.chunk_tiles, nkt);
+  const int kbeg = kt0 * kPrefillBN;
+  const int klim = min(kt1 * kPrefillBN, p.kv_len);                 // end before the causal limit
+  const int kend = p.causal ? min(klim, (qt + 1) * BM) : klim;
+  const int ntiles = (kend - kbeg + BN - 1) / BN;
   const float c = p.scale * kLog2e;
   const int row0 = qt * BM + wave * RB * 16;   // first query row of this wave
 
@@ -507,14 +519,21 @@ prefill_fa_kernel(const PrefillParams p) {
   struct Stage {
     u32x4 k[NV], v[NV];
   };
-  auto tile_of = [&](int j) { return min(kt0 + grp + KS * j, kt1 - 1); };
+  auto tile_of = [&](int j) { return min(grp + KS * j, ntiles - 1); };
+  // per-tile buffer resources: base at the tile's first row, range ending at
+  // the last key row, so rows past kv_len read as zero (byte quantities in
+  // scalar registers, one multiply per tile)
+  const char* kfirst = reinterpret_cast<const char*>(kbase + (size_t)kbeg * p.k_stride);
+  const char* vfirst = reinterpret_cast<const char*>(vbase + (size_t)kbeg * p.v_stride);
+  const unsigned long long kstep = (unsigned long long)BN * p.k_stride * sizeof(T);
+  const unsigned long long vstep = (unsigned long long)BN * p.v_stride * sizeof(T);
+  const unsigned long long kbytes = ((unsigned long long)(p.kv_len - 1 - kbeg) * p.k_stride + D) * sizeof(T);
+  const unsigned long long vbytes = ((unsigned long long)(p.kv_len - 1 - kbeg) * p.v_stride + D) * sizeof(T);
   auto gload = [&](int j, Stage& s) {
-    const int k0 = tile_of(j) * BN;
-    const long long rows = p.kv_len - k0;   // >= 1
-    const __amdgpu_buffer_rsrc_t rk =
-        make_rsrc(kbase + (size_t)k0 * p.k_stride, (unsigned long long)((rows - 1) * p.k_stride + D) * sizeof(T));
-    const __amdgpu_buffer_rsrc_t rv =
-        make_rsrc(vbase + (size_t)k0 * p.v_stride, (unsigned long long)((rows - 1) * p.v_stride + D) * sizeof(T));
+    const unsigned t = (unsigned)tile_of(j);
+    const unsigned long long ko = t * kstep, vo = t * vstep;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kfirst + ko, kbytes - ko);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vfirst + vo, vbytes - vo);
 #pragma unroll
     for (int i = 0; i < NV; ++i) s.k[i] = buffer_load16(rk, koff[i], 0);
 #pragma unroll
@@ -542,19 +561,19 @@ prefill_fa_kernel(const PrefillParams p) {
   }
   const u32x4 ones = u32x4{kOnes2<T>, kOnes2<T>, kOnes2<T>, kOnes2<T>};
 
-  auto compute = [&](int b, int kt) {
+  auto compute = [&](int b, int t) {
     const uint16_t* sk = tiles + b * BUF;
     const uint16_t* sv = sk + SKT;
-    const int k0 = kt * BN;
-    u32x4 kf[4][KSD];
+    const int k0 = kbeg + t * BN;
+    u32x4 kf[KB][KSD];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int ks = 0; ks < KSD; ++ks)
         kf[kb][ks] = *reinterpret_cast<const u32x4*>(sk + (kb * 16 + col) * KP + ks * 32 + g * 8);
-    f32x4 st[RB][4];
+    f32x4 st[RB][KB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         st[r][kb] = mfma16x16x32<T>(kf[kb][0], qf[r][0], negm[r]);
@@ -562,9 +581,9 @@ prefill_fa_kernel(const PrefillParams p) {
         for (int ks = 1; ks < KSD; ++ks) st[r][kb] = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], st[r][kb]);
       }
     // V^T fragments: rows (keys) ks2*32 + 4g + (col >> 2) (+16), columns db*16 + 4 (col & 3)
-    u32x4 vf[DB][2];
+    u32x4 vf[DB][BN / 32];
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2)
+    for (int ks2 = 0; ks2 < BN / 32; ++ks2)
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const uint16_t* a = sv + (ks2 * 32 + 4 * g + (col >> 2)) * VP + db * 16 + 4 * (col & 3);
@@ -572,12 +591,12 @@ prefill_fa_kernel(const PrefillParams p) {
         const u32x2 hi = lds_read_tr16(a + 16 * VP);
         vf[db][ks2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
-    if (!(k0 + BN <= p.kv_len && (!p.causal || k0 + BN - 1 <= row0))) {
+    if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0))) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        const int lim = p.causal ? min(p.kv_len - 1, qi[r]) : p.kv_len - 1;   // last visible key
+        const int lim = p.causal ? min(klim - 1, qi[r]) : klim - 1;   // last visible key
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             st[r][kb][i] = k0 + kb * 16 + 4 * g + i <= lim ? st[r][kb][i] : kNegInf;
@@ -587,7 +606,7 @@ prefill_fa_kernel(const PrefillParams p) {
     bool need_any = false;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      mt[r] = max_over_g(max16(st[r]));
+      mt[r] = max_over_g(max_tile<KB>(st[r]));
       need_any = need_any || mt[r] > thr[r];
     }
     if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
@@ -600,23 +619,23 @@ prefill_fa_kernel(const PrefillParams p) {
 #pragma unroll
         for (int db = 0; db <= DB; ++db) oacc[r][db] *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) st[r][kb] -= delta;
+        for (int kb = 0; kb < KB; ++kb) st[r][kb] -= delta;
         mref[r] += delta;
         negm[r] = f32x4{-mref[r], -mref[r], -mref[r], -mref[r]};
         thr[r] = need ? 8.0f : thr[r];
       }
     }
-    u32x4 pf[RB][2];
+    u32x4 pf[RB][BN / 32];
 #pragma unroll
     for (int r = 0; r < RB; ++r)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
+      for (int kb = 0; kb < KB; ++kb) {
         // reduction index 8g + j: key 4g + j of block 2 ks2 (j < 4), 4g + j - 4 of block 2 ks2 + 1
         pf[r][kb >> 1][(kb & 1) * 2] = pack2<T>(fast_exp2(st[r][kb][0]), fast_exp2(st[r][kb][1]));
         pf[r][kb >> 1][(kb & 1) * 2 + 1] = pack2<T>(fast_exp2(st[r][kb][2]), fast_exp2(st[r][kb][3]));
       }
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2)
+    for (int ks2 = 0; ks2 < BN / 32; ++ks2)
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
 #pragma unroll
@@ -625,9 +644,9 @@ prefill_fa_kernel(const PrefillParams p) {
       }
   };
 
-  // group tile sequence kt0 + grp + KS j; steps padded to even so the loop body
+  // group tile sequence grp + KS j; steps padded to even so the loop body
   // (two steps, one per LDS buffer) has no exit and the same loads on every path
-  const int nsteps = (kt1 - kt0 + KS - 1) / KS;
+  const int nsteps = (ntiles + KS - 1) / KS;
   const int nsteps2 = (nsteps + 1) & ~1;
   Stage sa, sb;
   gload(0, sa);
@@ -636,11 +655,11 @@ prefill_fa_kernel(const PrefillParams p) {
   gload(2, sa);
   lds_barrier();
   for (int j = 0; j < nsteps2; j += 2) {
-    if (kt0 + grp + KS * j < kt1) compute(0, kt0 + grp + KS * j);
+    if (grp + KS * j < ntiles) compute(0, grp + KS * j);
     lstore(sb, 1);
     gload(j + 3, sb);
     lds_barrier();
-    if (kt0 + grp + KS * (j + 1) < kt1) compute(1, kt0 + grp + KS * (j + 1));
+    if (grp + KS * (j + 1) < ntiles) compute(1, grp + KS * (j + 1));
     lstore(sa, 0);
     gload(j + 4, sa);
     lds_barrier();
@@ -648,14 +667,14 @@ prefill_fa_kernel(const PrefillParams p) {
 
   float mfin[RB], lfin[RB];
   if constexpr (KS > 1) {
-    float* so = reinterpret_cast<float*>(smem);   // [KS][64 rows][D]
-    float* ssum = so + KS * BM * D;               // [KS][64 rows]
+    float* so = reinterpret_cast<float*>(smem);   // [KS][64 rows][MP]
+    float* ssum = so + KS * BM * MP;              // [KS][64 rows]
     float* smax = ssum + KS * BM;                 // [KS][64 rows]
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const int row = (wave * RB + r) * 16 + col;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(&so[(grp * BM + row) * D + db * 16 + 4 * g]) = oacc[r][db];
+      for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(&so[(grp * BM + row) * MP + db * 16 + 4 * g]) = oacc[r][db];
       if (g == 0) {
         ssum[grp * BM + row] = oacc[r][DB][0];
         smax[grp * BM + row] = thr[r] > 0.0f ? mref[r] : kNegInf;
@@ -679,7 +698,7 @@ prefill_fa_kernel(const PrefillParams p) {
         L = fmaf(ssum[s * BM + row], f, L);
 #pragma unroll
         for (int db = 0; db < DB; ++db)
-          oacc[r][db] += *reinterpret_cast<const f32x4*>(&so[(s * BM + row) * D + db * 16 + 4 * g]) * f;
+          oacc[r][db] += *reinterpret_cast<const f32x4*>(&so[(s * BM + row) * MP + db * 16 + 4 * g]) * f;
       }
       mfin[r] = M;
       lfin[r] = L;
@@ -846,6 +865,20 @@ size_t prefill_workspace_bytes(const PrefillParams& p, int dtype) {
   return (size_t)p.num_heads * nqt * max_chunks * kPrefillBM * (p.head_dim + 2) * sizeof(float);
 }
 
+// head_dim 64 kernel shapes: 0 = 16-row waves, 2 key groups; 1 = 32-row
+// waves, 2 key groups; 2 = 32-row waves, 1 key group.
+template <typename T> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
+#ifdef TV_PREFILL_FIXED
+  (void)cfg;
+  hipLaunchKernelGGL((prefill_fa_kernel<T, 64, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN>), grid,
+                     dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
+#else
+  if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 2, 64>), grid, dim3(512), 0, stream, pp);
+  else if (cfg == 1) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 2, 2, 64>), grid, dim3(256), 0, stream, pp);
+  else hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 2, 1, 64>), grid, dim3(128), 0, stream, pp);
+#endif
+}
+
 // Returns 0 on launch, 1 if the shape has no kernel, 2 if the workspace is missing.
 int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, size_t workspace_bytes,
                          hipStream_t stream) {
@@ -875,14 +908,19 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
       else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
     }
 #else
-    constexpr int RB = TV_PREFILL_RB, KS = TV_PREFILL_KS;
-    const dim3 block(256 / RB * KS);
-    if (dtype == kF16) {
-      if (d64) hipLaunchKernelGGL((prefill_fa_kernel<_Float16, 64, RB, KS>), grid, block, 0, stream, pp);
-      else hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128, 1>), grid, dim3(256), 0, stream, pp);
+    if (d64) {
+      // Few work-groups (short prompts): 8 waves of one 16-row block each
+      // split the key tiles two ways, halving the longest chain.  Enough
+      // work-groups to fill the CUs twice: 32-row waves, still split.  More:
+      // unsplit 2-wave work-groups, no merge.
+      const long long wgs = (long long)grid.x * grid.y;
+      const int cfg = wgs <= 256 ? 0 : (wgs < 1024 ? 1 : 2);
+      if (dtype == kF16) launch_fa<_Float16>(cfg, grid, pp, stream);
+      else launch_fa<__bf16>(cfg, grid, pp, stream);
+    } else if (dtype == kF16) {
+      hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128, 1>), grid, dim3(256), 0, stream, pp);
     } else {
-      if (d64) hipLaunchKernelGGL((prefill_fa_kernel<__bf16, 64, RB, KS>), grid, block, 0, stream, pp);
-      else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
+      hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
     }
 #endif
     if (max_chunks > 1) {
