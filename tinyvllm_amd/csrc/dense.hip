@@ -39,7 +39,7 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 template <typename T, int EPI>
 __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const LinearParams p) {
-  constexpr int KP = kLinKC + 8;   // LDS pitch (elements): 16-byte reads of 16 rows hit distinct banks
+  constexpr int KP = kLinKC + 16;  // LDS pitch: 544 bytes, an odd multiple of 32 modulo 256 -- conflict-free 16-byte reads
   __shared__ __attribute__((aligned(16))) uint16_t sa[kLinBM * KP];
 
   const int tid = threadIdx.x;
