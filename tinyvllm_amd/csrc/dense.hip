@@ -36,11 +36,75 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 #ifndef TV_LINEAR_MIN_BLOCKS
 #define TV_LINEAR_MIN_BLOCKS 1
 #endif
+#ifndef TV_LINEAR_WSTAGES
+#define TV_LINEAR_WSTAGES 2
+#endif
+#ifndef TV_LINEAR_ASTAGES
+#define TV_LINEAR_ASTAGES 1
+#endif
+
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+constexpr int lcm3(int a, int b, int c) {
+  const int ab = a / gcd_c(a, b) * b;
+  return ab / gcd_c(ab, c) * c;
+}
+
+// Epilogue of the skinny product: lane (wave, g, col) holds acc[mb][i] =
+// Y[m0 + 16 mb + col][n_wave + 4 g + i].  sk: 8 KB of LDS for the argmax
+// exchange (logits), free to reuse once every wave reaches this point.
+template <typename T, int EPI>
+__device__ __forceinline__ void linear_epilogue(const LinearParams& p, const f32x4 (&acc)[4], int n_wave, int m0,
+                                                int split, int ntile, int wave, int tid, unsigned long long* sk) {
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+  const int n = n_wave + 4 * g;
+  if constexpr (EPI == kEpiPartial) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = m0 + mb * 16 + col;
+      if (m < p.M && n < p.N)
+        *reinterpret_cast<f32x4*>(p.part + ((size_t)split * p.M + m) * p.N + n) = acc[mb];
+    }
+  } else if constexpr (EPI == kEpiSwiglu) {
+    // rows 4j, 4j+1 of W are w1 rows 2j, 2j+1; rows 4j+2, 4j+3 the matching w3 rows
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = m0 + mb * 16 + col;
+      if (m < p.M && n < p.N) {
+        const f32x4 v = acc[mb];
+        const uint32_t h = pack2<T>(silu(v[0]) * v[2], silu(v[1]) * v[3]);
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)m * p.ldo + (n >> 1)) = h;
+      }
+    }
+  } else {
+    lds_barrier();   // sk reuses LDS of the main loop: [16 (wave, g)][64 rows]
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int m = m0 + mb * 16 + col;
+      const f32x4 v = acc[mb];
+      if (p.out && m < p.M && n < p.N)
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (size_t)m * p.ldo + n) = v;
+      unsigned long long best = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < p.N) best = max(best, argmax_key(v[i], n + i));
+      sk[(wave * 4 + g) * 64 + mb * 16 + col] = best;
+    }
+    lds_barrier();
+    if (tid < 64 && p.keys && m0 + tid < p.M) {
+      unsigned long long best = sk[tid];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) best = max(best, sk[j * 64 + tid]);
+      p.keys[(size_t)ntile * p.M + m0 + tid] = best;
+    }
+  }
+}
 
 template <typename T, int EPI>
 __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const LinearParams p) {
   constexpr int KP = kLinKC + 16;  // LDS pitch: 544 bytes, an odd multiple of 32 modulo 256 -- conflict-free 16-byte reads
-  __shared__ __attribute__((aligned(16))) uint16_t sa[kLinBM * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t sa[2][kLinBM * KP];   // A chunk, double-buffered
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: W resource in SGPRs
@@ -94,10 +158,10 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = buffer_load16(ares, off, i * a_rows8);
   };
-  auto storeA = [&](const u32x4 (&r)[8], bool valid) {
+  auto storeA = [&](const u32x4 (&r)[8], bool valid, int buf) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<u32x4*>(&sa[((tid >> 5) + 8 * i) * KP + 8 * (tid & 31)]) = valid ? r[i] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&sa[buf][((tid >> 5) + 8 * i) * KP + 8 * (tid & 31)]) = valid ? r[i] : u32x4{0, 0, 0, 0};
   };
 
   f32x4 acc[4];
@@ -105,108 +169,71 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
   for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   // All 8 k steps run even on a partial chunk: the A rows there are zero.
   // The B fragments of step s + 1 are read from LDS while step s multiplies.
-  auto compute = [&](const u32x4 (&r)[8]) {
+  auto compute = [&](const u32x4 (&r)[8], int buf) {
     u32x4 b[2][4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) b[0][mb] = *reinterpret_cast<const u32x4*>(&sa[(mb * 16 + col) * KP + 8 * g]);
+    for (int mb = 0; mb < 4; ++mb) b[0][mb] = *reinterpret_cast<const u32x4*>(&sa[buf][(mb * 16 + col) * KP + 8 * g]);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       if (s + 1 < 8) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
-          b[(s + 1) & 1][mb] = *reinterpret_cast<const u32x4*>(&sa[(mb * 16 + col) * KP + 32 * (s + 1) + 8 * g]);
+          b[(s + 1) & 1][mb] = *reinterpret_cast<const u32x4*>(&sa[buf][(mb * 16 + col) * KP + 32 * (s + 1) + 8 * g]);
       }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma16x16x32<T>(r[s], b[s & 1][mb], acc[mb]);
     }
   };
 
-  u32x4 w0[8], w1[8], ar[8];
-  bool av;
-  loadW(0, w0);
-  loadA(0, ar, av);
+  constexpr int NWS = TV_LINEAR_WSTAGES;   // W chunks in registers: in flight + the one multiplied
+  constexpr int NAS = TV_LINEAR_ASTAGES;   // A chunks in flight in registers
+  constexpr int U = lcm3(NWS, NAS, 2);     // loop unroll: every stage / buffer index compile-time
+  u32x4 w[NWS][8], ar[NAS][8];
+  bool av[NAS];
   if (nc == 1) {
-    storeA(ar, av);
+    loadW(0, w[0]);
+    loadA(0, ar[0], av[0]);
+    storeA(ar[0], av[0], 0);
     lds_barrier();
-    compute(w0);
+    compute(w[0], 0);
   } else {
-    // W and A of chunk c + 1 are in flight while chunk c computes.  The loads
-    // are unconditional and the step count is padded to even (the padding step
-    // multiplies zero A rows), so the loop body has no exit and the compiler
-    // waits for exactly the chunk it needs.
-    // (sched_barrier keeps each prefetch issued before the waits that follow)
-    const int ncp = (nc + 1) & ~1;
-    for (int c = 0; c < ncp; c += 2) {
-      loadW(c + 1, w1);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_barrier();
-      storeA(ar, av);
-      lds_barrier();
-      loadA(c + 1, ar, av);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(w0);
-      loadW(c + 2, w0);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_barrier();
-      storeA(ar, av);
-      lds_barrier();
-      loadA(c + 2, ar, av);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(w1);
-    }
-  }
-
-  // lane holds acc[mb][i] = Y[m0 + 16 mb + col][n_wave + 4 g + i]
-  const int n = n_wave + 4 * g;
-  if constexpr (EPI == kEpiPartial) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int m = m0 + mb * 16 + col;
-      if (m < p.M && n < p.N)
-        *reinterpret_cast<f32x4*>(p.part + ((size_t)split * p.M + m) * p.N + n) = acc[mb];
-    }
-  } else if constexpr (EPI == kEpiSwiglu) {
-    // rows 4j, 4j+1 of W are w1 rows 2j, 2j+1; rows 4j+2, 4j+3 the matching w3 rows
+    for (int i = 0; i < NWS - 1; ++i) loadW(i, w[i]);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int m = m0 + mb * 16 + col;
-      if (m < p.M && n < p.N) {
-        const f32x4 v = acc[mb];
-        const uint32_t h = pack2<T>(silu(v[0]) * v[2], silu(v[1]) * v[3]);
-        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)m * p.ldo + (n >> 1)) = h;
+    for (int i = 0; i < NAS; ++i) loadA(i, ar[i], av[i]);
+    // Step j multiplies chunk j: W of chunks j + 1 .. j + NWS - 1 and A of
+    // chunks j + 1 .. j + NAS are in flight meanwhile.  A goes through two
+    // LDS buffers, so one barrier per step orders both its store and the
+    // reuse of the buffer two steps later.  The loads are unconditional and
+    // the step count is padded to a multiple of U (padding steps multiply
+    // zero A rows), so the loop body has no exit and the compiler waits for
+    // exactly the chunk it needs.  (sched_barrier keeps each prefetch issued
+    // before the waits that follow.)
+    const int ncp = (nc + U - 1) / U * U;
+    for (int c = 0; c < ncp; c += U) {
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        loadW(c + j + NWS - 1, w[(j + NWS - 1) % NWS]);
+        __builtin_amdgcn_sched_barrier(0);
+        storeA(ar[j % NAS], av[j % NAS], j & 1);
+        lds_barrier();
+        loadA(c + j + NAS, ar[j % NAS], av[j % NAS]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(w[j % NWS], j & 1);
       }
     }
-  } else {
-    lds_barrier();   // the A chunk buffer is reused for the argmax exchange
-    unsigned long long* sk = reinterpret_cast<unsigned long long*>(sa);   // [16 (wave, g)][64 rows]
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int m = m0 + mb * 16 + col;
-      const f32x4 v = acc[mb];
-      if (p.out && m < p.M && n < p.N)
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + (size_t)m * p.ldo + n) = v;
-      unsigned long long best = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (n + i < p.N) best = max(best, argmax_key(v[i], n + i));
-      sk[(wave * 4 + g) * 64 + mb * 16 + col] = best;
-    }
-    lds_barrier();
-    if (tid < 64 && p.keys && m0 + tid < p.M) {
-      unsigned long long best = sk[tid];
-#pragma unroll
-      for (int j = 1; j < 16; ++j) best = max(best, sk[j * 64 + tid]);
-      p.keys[(size_t)ntile * p.M + m0 + tid] = best;
-    }
   }
+
+  linear_epilogue<T, EPI>(p, acc, n_wave, m0, split, ntile, wave, tid, reinterpret_cast<unsigned long long*>(&sa[0][0]));
 }
 
-#define TV_LINEAR_CASE(T)                                                                           \
-  switch (epi) {                                                                                    \
+
+#define TV_LINEAR_CASE(T)                                                                              \
+  switch (epi) {                                                                                       \
     case kEpiPartial: hipLaunchKernelGGL((linear_kernel<T, kEpiPartial>), grid, dim3(256), 0, s, p); \
-      break;                                                                                        \
+      break;                                                                                           \
     case kEpiSwiglu: hipLaunchKernelGGL((linear_kernel<T, kEpiSwiglu>), grid, dim3(256), 0, s, p);   \
-      break;                                                                                        \
+      break;                                                                                           \
     default: hipLaunchKernelGGL((linear_kernel<T, kEpiLogits>), grid, dim3(256), 0, s, p);           \
   }
 
