@@ -396,14 +396,6 @@ __global__ void __launch_bounds__(256 * KSPLIT) prefill_mfma_kernel(const Prefil
 // and loaded two steps ahead through buffer loads whose range ends at the last
 // key row (rows past kv_len read as zero), one barrier per step.
 
-// ds_read_b64_tr_b16: within each 16-lane row of the wave, lane i receives
-// element i % 4 of the 64-bit words addressed by lanes 4 k + i / 4, k = 0..3.
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* ptr) {
-  typedef short v4s __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4s lds_v4s;
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(ptr)));
-}
-
 template <typename T> __device__ __forceinline__ u32x4 scale8(u32x4 w, float c) {
   u32x4 r;
 #pragma unroll

@@ -26,9 +26,10 @@ template <typename T, int D, int NW, int PF>
 __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams p) {
   constexpr int KS = D / 32;        // MFMA k steps over the head dim
   constexpr int DB = D / 16;        // 16-dim blocks of O^T
-  constexpr int VP = 32 + 4;        // LDS pitch (tokens) of a wave's V^T tile: 8-byte reads of 16 rows hit distinct banks
-  constexpr int VU = D / 32;        // (token pair, 8-dim chunk) V units per lane per tile
-  constexpr int SVT = NW * D * VP;  // V^T tiles of all waves (elements)
+  constexpr int VP = D + 16;        // V tile row pitch (2 D + 32 bytes): conflict-free transposing reads
+  constexpr int CPR = D / 8;        // 16-byte chunks per row
+  constexpr int VU = 32 * CPR / 64; // V (token, chunk) units per lane per tile
+  constexpr int SVT = NW * 32 * VP; // V tiles of all waves (elements)
   constexpr int SO = NW * 16 * D * 2;   // merge buffer [NW][16][D] floats, in elements
   constexpr int UNION = SVT > SO ? SVT : SO;
   __shared__ __attribute__((aligned(16))) uint16_t smem[16 * D + UNION];
@@ -36,7 +37,7 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   __shared__ float sm[NW][16];
   __shared__ float sl[NW][16];
   uint16_t* sq = smem;                       // [16 heads][D] query rows, heads >= G zero
-  uint16_t* svt = smem + 16 * D;
+  uint16_t* svt = smem + 16 * D;      // [NW][32 tokens][VP] row-major V tiles
 
   const int kvh = blockIdx.x;
   const int b = blockIdx.y;
@@ -67,6 +68,49 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
     return bt[min(tok / bs, p.max_blocks - 1)];
   };
   int blkv = load_blocks(0);
+
+  struct Tile {
+    u32x4 k[2][KS];
+    u32x4 v[VU];
+    int t0;
+    bool ok0, ok1;
+  };
+  // Tile j of this wave: tokens t0 .. t0+31, two 16-token halves each inside
+  // one cache block (block_size is a multiple of 16).
+  // (j - j0 < 32: the block ids of tiles j0 .. j0+31 are in blkv)
+  auto load = [&](int j, int j0, Tile& r) {
+    const int t0 = (wave + NW * j) * 32;
+    r.t0 = t0;
+    int b0 = __builtin_amdgcn_readlane(blkv, 2 * (j - j0));
+    int b1 = __builtin_amdgcn_readlane(blkv, 2 * (j - j0) + 1);
+    r.ok0 = (unsigned)b0 < (unsigned)p.num_blocks;
+    r.ok1 = (unsigned)b1 < (unsigned)p.num_blocks;
+    b0 = r.ok0 ? b0 : 0;
+    b1 = r.ok1 ? b1 : 0;
+    const size_t base0 = ((size_t)b0 * bs + t0 % bs) * rs;
+    const size_t base1 = ((size_t)b1 * bs + (t0 + 16) % bs) * rs;
+    // K rows: lane (token col of the half, 8-dim group g)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      r.k[0][ks] = *reinterpret_cast<const u32x4*>(kcache + base0 + col * rs + 32 * ks + 8 * g);
+      r.k[1][ks] = *reinterpret_cast<const u32x4*>(kcache + base1 + col * rs + 32 * ks + 8 * g);
+    }
+    // V rows: unit (token, 16-byte chunk), staged row-major in LDS
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int unit = lane + 64 * i;
+      const int tok = unit / CPR;
+      const int ch = unit % CPR;
+      r.v[i] = *reinterpret_cast<const u32x4*>(vcache + (tok < 16 ? base0 : base1) + (size_t)(tok & 15) * rs + 8 * ch);
+    }
+  };
+
+  // The first tiles' K / V loads depend only on the block table: issue them
+  // before the q / k / v prologue so their latency overlaps it (tile 0 of the
+  // wave is a valid address even when the wave has no tile; it is not used).
+  Tile t[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load(min(i, max(nt, 1) - 1), 0, t[i]);
 
   // ---- q, k, v of the new token -----------------------------------------
   long long slot = -1;
@@ -129,45 +173,7 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   f32x4 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint16_t* vt = svt + wave * (D * VP);
-
-  struct Tile {
-    u32x4 k[2][KS];
-    u32x4 v[VU][2];
-    int t0;
-    bool ok0, ok1;
-  };
-  // Tile j of this wave: tokens t0 .. t0+31, two 16-token halves each inside
-  // one cache block (block_size is a multiple of 16).
-  // (j - j0 < 32: the block ids of tiles j0 .. j0+31 are in blkv)
-  auto load = [&](int j, int j0, Tile& r) {
-    const int t0 = (wave + NW * j) * 32;
-    r.t0 = t0;
-    int b0 = __builtin_amdgcn_readlane(blkv, 2 * (j - j0));
-    int b1 = __builtin_amdgcn_readlane(blkv, 2 * (j - j0) + 1);
-    r.ok0 = (unsigned)b0 < (unsigned)p.num_blocks;
-    r.ok1 = (unsigned)b1 < (unsigned)p.num_blocks;
-    b0 = r.ok0 ? b0 : 0;
-    b1 = r.ok1 ? b1 : 0;
-    const size_t base0 = ((size_t)b0 * bs + t0 % bs) * rs;
-    const size_t base1 = ((size_t)b1 * bs + (t0 + 16) % bs) * rs;
-    // K rows: lane (token col of the half, 8-dim group g)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      r.k[0][ks] = *reinterpret_cast<const u32x4*>(kcache + base0 + col * rs + 32 * ks + 8 * g);
-      r.k[1][ks] = *reinterpret_cast<const u32x4*>(kcache + base1 + col * rs + 32 * ks + 8 * g);
-    }
-    // V rows: lane (token pair tp, 8-dim chunk ch)
-#pragma unroll
-    for (int i = 0; i < VU; ++i) {
-      const int unit = lane + 64 * i;
-      const int tp = unit & 15;
-      const int ch = unit >> 4;
-      const size_t base = (tp < 8 ? base0 : base1) + (size_t)(2 * (tp & 7)) * rs + 8 * ch;
-      r.v[i][0] = *reinterpret_cast<const u32x4*>(vcache + base);
-      r.v[i][1] = *reinterpret_cast<const u32x4*>(vcache + base + rs);
-    }
-  };
+  uint16_t* vt = svt + wave * (32 * VP);
 
   auto consume = [&](Tile& r) {
     if (p.write_before && r.t0 <= pos && pos < r.t0 + 32) {
@@ -181,10 +187,7 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
 #pragma unroll
       for (int i = 0; i < VU; ++i) {
         const int unit = lane + 64 * i;
-        const int tok = r.t0 + 2 * (unit & 15);
-        const u32x4 nv = *reinterpret_cast<const u32x4*>(&snew[D / 2 + 4 * (unit >> 4)]);
-        if (tok == pos) r.v[i][0] = nv;
-        if (tok + 1 == pos) r.v[i][1] = nv;
+        if (r.t0 + unit / CPR == pos) r.v[i] = *reinterpret_cast<const u32x4*>(&snew[D / 2 + 4 * (unit % CPR)]);
       }
     }
     // S^T: st[tb][i] = q_head(col) . k(token t0 + 16 tb + 4 g + i)
@@ -234,32 +237,23 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
     // token 16 + 4 g + j - 4 for j >= 4, on both MFMA operands
     const u32x4 pf = u32x4{pack2<T>(e[0][0], e[0][1]), pack2<T>(e[0][2], e[0][3]), pack2<T>(e[1][0], e[1][1]),
                            pack2<T>(e[1][2], e[1][3])};
-    // V^T tile: vt[dim][token] as 32-bit token pairs (rows of masked tokens are zeroed)
+    // V tile rows in LDS (rows of masked tokens zeroed), read back as the V^T
+    // operand by transposing reads: rows 4 g + (col >> 2) (+16), columns
+    // db * 16 + 4 (col & 3) give lane (g, col) V[token(8 g + j)][db * 16 + col]
 #pragma unroll
     for (int i = 0; i < VU; ++i) {
       const int unit = lane + 64 * i;
-      const int tp = unit & 15;
-      const int ch = unit >> 4;
-      u32x4 v0 = r.v[i][0], v1 = r.v[i][1];
-      if (partial) {
-        const int tok = r.t0 + 2 * tp;
-        const bool okb = tp < 8 ? r.ok0 : r.ok1;
-        if (!okb || tok >= len) v0 = u32x4{0, 0, 0, 0};
-        if (!okb || tok + 1 >= len) v1 = u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        uint16_t* dst = &vt[(8 * ch + 2 * w) * VP + 2 * tp];
-        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(dst + VP) = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
-      }
+      const int tok = unit / CPR;
+      u32x4 v = r.v[i];
+      if (partial && (!(tok < 16 ? r.ok0 : r.ok1) || r.t0 + tok >= len)) v = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&vt[tok * VP + 8 * (unit % CPR)]) = v;
     }
     // O^T += V^T P^T
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const uint16_t* row = &vt[(db * 16 + col) * VP + 4 * g];
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+      const uint16_t* a = &vt[(4 * g + (col >> 2)) * VP + db * 16 + 4 * (col & 3)];
+      const u32x2 lo = lds_read_tr16(a);
+      const u32x2 hi = lds_read_tr16(a + 16 * VP);
       o[db] = mfma16x16x32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, o[db]);
     }
   };
@@ -268,11 +262,12 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   // tiles are in flight and the loads are unconditional (the chunk's last tile
   // is re-read) so the compiler waits for exactly the tile it consumes.
   for (int j0 = 0; j0 < nt; j0 += 32) {
-    if (j0 > 0) blkv = load_blocks(j0);
     const int je = min(nt, j0 + 32);
-    Tile t[PF];
+    if (j0 > 0) {
+      blkv = load_blocks(j0);
 #pragma unroll
-    for (int i = 0; i < PF; ++i) load(min(j0 + i, je - 1), j0, t[i]);
+      for (int i = 0; i < PF; ++i) load(min(j0 + i, je - 1), j0, t[i]);
+    }
     int j = j0;
     for (; j + PF - 1 < je; j += PF) {
 #pragma unroll

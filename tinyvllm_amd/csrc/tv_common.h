@@ -173,6 +173,17 @@ template <int N> __device__ __forceinline__ float group_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane row of the wave, lane i
+// receives element i % 4 of the 64-bit words addressed by lanes 4 k + i / 4,
+// k = 0..3.  With lane 4 k + q addressing row r_k, columns c + 4 q .. c + 4 q + 3
+// of a row-major 16-bit matrix, lane i gets column c + i of rows r_0 .. r_3:
+// a 4 x 16 block transposed into the MFMA operand layout.  ptr: LDS address.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* ptr) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(ptr)));
+}
+
 // Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit dwords, no
 // swizzle).  A load whose voffset lies at or past `bytes` returns zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned long long bytes) {
