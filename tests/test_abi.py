@@ -113,11 +113,12 @@ def test_no_bit_cast_of_vector_element_lvalues():
 
 
 def test_linear_split_choice():
-    """K splits the decode step uses: about one work-group per CU, whole 256-wide
-    K chunks, and one split once the output tiles alone fill the GPU."""
+    """K splits the decode step uses: about 192 work-groups, whole 256-wide K
+    chunks, and one split once the output tiles alone fill half of that."""
     lib = _lib.load()
-    assert lib.tv_linear_k_split(64, 2560, 2048) == 256        # q|k|v: 40 tiles x 8 splits
-    assert lib.tv_linear_k_split(64, 2048, 5632) == 768        # down projection
+    assert lib.tv_linear_k_split(64, 2560, 2048) == 512        # q|k|v: 40 tiles x 4 splits
+    assert lib.tv_linear_k_split(64, 2048, 2048) == 256        # output projection: 32 tiles x 8 splits
+    assert lib.tv_linear_k_split(64, 2048, 5632) == 1024       # down projection: 32 tiles x 6 splits
     assert lib.tv_linear_k_split(64, 11264, 2048) == 2048      # w1|w3: 176 tiles, one split
     assert lib.tv_linear_k_split(1024, 2560, 2048) == 2048     # prefill rows fill the GPU
     assert lib.tv_linear_k_split(4, 96, 64) % 32 == 0
