@@ -50,7 +50,7 @@ const char* tv_last_error(void);
  * Workspace (bytes) needed by tv_paged_decode for the split-context partials:
  * num_seqs * num_heads * ceil(max_blocks*block_size / partition_size)
  * * (head_dim + 2) floats.  When every sequence fits one partition and
- * num_seqs >= 32 it is num_seqs ints (rounded up to 256 bytes) for a
+ * 32 <= num_seqs <= 1024 it is num_seqs ints (rounded up to 256 bytes) for a
  * longest-first schedule of the sequences, which tv_paged_decode uses when
  * the caller provides it and skips otherwise; else 0.  Host-only computation.
  */

@@ -469,8 +469,8 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
 // grid (Hq, B) and 64 threads; sequences that fit one partition were written by
 // the main kernel and are skipped here.
 __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodeParams p, int head_dim);
-__global__ void __launch_bounds__(256) decode_order_kernel(const int* context_lens, int num_seqs, int width,
-                                                           int* order);
+__global__ void __launch_bounds__(1024) decode_order_kernel(const int* context_lens, int num_seqs, int width,
+                                                            int* order);
 
 
 }  // namespace tv

@@ -66,30 +66,41 @@ __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodePar
   }
 }
 
-// Longest-first schedule of an unsplit decode launch: order[rank] = b, where
-// rank counts the sequences that attend to more positions than b (ties by
-// index).  Work-groups are dispatched in grid order, so the longest sequences
-// start first and the last ones to start are short: the launch does not end
-// on a few long sequences streaming while most CUs idle.  Any permutation is
-// correct; this one only shortens the tail.  grid ceil(B / 256), 256 threads.
-__global__ void __launch_bounds__(256) decode_order_kernel(const int* context_lens, int num_seqs, int width,
-                                                           int* order) {
-  __shared__ int sl[256];
-  const int b = blockIdx.x * 256 + threadIdx.x;
-  auto eff = [&](int ctx) { return ctx <= 0 ? width : (ctx < width ? ctx : width); };
-  const int mine = b < num_seqs ? eff(context_lens[b]) : 0;
-  int rank = 0;
-  for (int base = 0; base < num_seqs; base += 256) {
-    __syncthreads();
-    if (base + (int)threadIdx.x < num_seqs) sl[threadIdx.x] = eff(context_lens[base + threadIdx.x]);
-    __syncthreads();
-    const int n = min(256, num_seqs - base);
-    for (int j = 0; j < n; ++j) {
-      const int lj = sl[j];
-      rank += (lj > mine) || (lj == mine && base + j < b);
-    }
+// Longest-first schedule of an unsplit decode launch: order[rank] = b.
+// Sequences are ranked by 16 length classes (attended length * 16 / (width + 1)),
+// longest class first, batch order inside a class -- one ballot per class and
+// wave instead of a full sort.  Work-groups are dispatched in grid order, so
+// the longest sequences start first and the last ones to start are short: the
+// launch does not end on a few long sequences streaming while most CUs idle.
+// Any permutation is correct; this one only shortens the tail.  One
+// work-group of 1024 threads, num_seqs <= 1024.
+__global__ void __launch_bounds__(1024) decode_order_kernel(const int* context_lens, int num_seqs, int width,
+                                                            int* order) {
+  constexpr int NC = 16;
+  __shared__ int cnt[16][NC];   // [wave][class] members
+  const int b = threadIdx.x;
+  const int wave = b >> 6, lane = b & 63;
+  int cls = -1;
+  if (b < num_seqs) {
+    const int ctx = context_lens[b];
+    const int len = ctx <= 0 ? width : (ctx < width ? ctx : width);
+    cls = (int)((long long)len * NC / ((long long)width + 1));
   }
-  if (b < num_seqs) order[rank] = b;
+  int before = 0;   // members of my class in my wave below my lane
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const unsigned long long m = __builtin_amdgcn_ballot_w64(cls == k);
+    if (lane == 0) cnt[wave][k] = __builtin_popcountll(m);
+    if (cls == k) before = __builtin_popcountll(m & ((1ull << lane) - 1));
+  }
+  __syncthreads();
+  if (b >= num_seqs) return;
+  int rank = before;
+  for (int w = 0; w < 16; ++w) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) rank += (k > cls || (k == cls && w < wave)) ? cnt[w][k] : 0;
+  }
+  order[rank] = b;
 }
 
 }  // namespace tv

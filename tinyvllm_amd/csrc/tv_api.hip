@@ -87,9 +87,10 @@ int tv_abi_version(void) { return 3; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
-// Unsplit launches of at least this many sequences run longest first
-// (decode_order_kernel), which needs num_seqs ints of workspace.
+// Unsplit launches of kDecodeOrderMinSeqs .. kDecodeOrderMaxSeqs sequences run
+// longest first (decode_order_kernel), which needs num_seqs ints of workspace.
 static constexpr int kDecodeOrderMinSeqs = 32;
+static constexpr int kDecodeOrderMaxSeqs = 1024;
 
 size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim, int max_blocks,
                                        int block_size, int partition_size) {
@@ -98,7 +99,10 @@ size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim
     return 0;
   const long long width = (long long)max_blocks * block_size;
   const long long parts = (width + partition_size - 1) / partition_size;
-  if (parts <= 1) return num_seqs >= kDecodeOrderMinSeqs ? ((size_t)num_seqs * sizeof(int) + 255) & ~(size_t)255 : 0;
+  if (parts <= 1)
+    return num_seqs >= kDecodeOrderMinSeqs && num_seqs <= kDecodeOrderMaxSeqs
+               ? ((size_t)num_seqs * sizeof(int) + 255) & ~(size_t)255
+               : 0;
   return (size_t)num_seqs * num_heads * parts * (head_dim + 2) * sizeof(float);
 }
 
@@ -173,8 +177,8 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (ordered) {
     p.order = reinterpret_cast<int*>(workspace);
-    hipLaunchKernelGGL(tv::decode_order_kernel, dim3((num_seqs + 255) / 256), dim3(256), 0, s, context_lens,
-                       num_seqs, (int)width, reinterpret_cast<int*>(workspace));
+    hipLaunchKernelGGL(tv::decode_order_kernel, dim3(1), dim3(1024), 0, s, context_lens, num_seqs, (int)width,
+                       reinterpret_cast<int*>(workspace));
   }
   const dim3 grid(max_parts, num_kv_heads * p.head_chunks, num_seqs);
   bool launched = false;
