@@ -860,8 +860,14 @@ size_t prefill_workspace_bytes(const PrefillParams& p, int dtype) {
   return (size_t)p.num_heads * nqt * max_chunks * kPrefillBM * (p.head_dim + 2) * sizeof(float);
 }
 
-// head_dim 64 kernel shapes: 0 = 16-row waves, 2 key groups; 1 = 32-row
-// waves, 2 key groups; 2 = 32-row waves, 1 key group.
+// Key tiles of the last query tile (the longest causal row), host side.
+int prefill_key_tiles_host(const PrefillParams& p, int qt) {
+  const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM) : p.kv_len;
+  return (kend + kPrefillBN - 1) / kPrefillBN;
+}
+
+// head_dim 64 kernel shapes: 0 = 16-row waves, 2 key groups (512 threads);
+// 1 = 16-row waves, 1 key group (256 threads).
 template <typename T> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
 #ifdef TV_PREFILL_FIXED
   (void)cfg;
@@ -869,8 +875,7 @@ template <typename T> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp
                      dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
 #else
   if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 2, 64>), grid, dim3(512), 0, stream, pp);
-  else if (cfg == 1) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 2, 2, 64>), grid, dim3(256), 0, stream, pp);
-  else hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 2, 1, 64>), grid, dim3(128), 0, stream, pp);
+  else hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 1, 64>), grid, dim3(256), 0, stream, pp);
 #endif
 }
 
@@ -904,12 +909,13 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     }
 #else
     if (d64) {
-      // Few work-groups (short prompts): 8 waves of one 16-row block each
-      // split the key tiles two ways, halving the longest chain.  Enough
-      // work-groups to fill the CUs twice: 32-row waves, still split.  More:
-      // unsplit 2-wave work-groups, no merge.
+      // One work-group per CU or fewer, with rows of 8+ key tiles: two key
+      // groups of 4 waves halve the longest chain (the idle SIMDs would wait
+      // anyway).  Otherwise 4 waves, no split and no merge.  (Measured at
+      // Hq 32: L = 64 / 256 / 512 / 1024 / 2048 take 4.2 / 6.0 / 7.9 / 14.5 /
+      // 35 us; 32-row waves were slower at every length.)
       const long long wgs = (long long)grid.x * grid.y;
-      const int cfg = wgs <= 256 ? 0 : (wgs < 1024 ? 1 : 2);
+      const int cfg = (wgs <= 256 && prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8) ? 0 : 1;
       if (dtype == kF16) launch_fa<_Float16>(cfg, grid, pp, stream);
       else launch_fa<__bf16>(cfg, grid, pp, stream);
     } else if (dtype == kF16) {
