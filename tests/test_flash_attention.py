@@ -117,6 +117,17 @@ def test_tinyllama_prefill_config2(length):
     check(q, k, v)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("lq,lk,causal", [(600, 600, False), (520, 520, True), (500, 700, True), (480, 900, False)])
+def test_key_split_work_groups(dtype, lq, lk, causal):
+    """Grids of at most one work-group per CU with rows of 8+ key tiles run two
+    key groups per work-group and merge them in LDS (head_dim 64)."""
+    q = randn(70, lq, 8, 64, dtype=dtype)
+    k = randn(71, lk, 2, 64, dtype=dtype)
+    v = randn(72, lk, 2, 64, dtype=dtype)
+    check(q, k, v, causal)
+
+
 def test_unequal_lengths_top_left_causal():
     q = randn(40, 40, 8, 64, dtype=torch.float16)
     k = randn(41, 100, 2, 64, dtype=torch.float16)
