@@ -127,8 +127,9 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
   auto chunk_of = [&](int i) { const int c = i + rot; return c < nc ? c : c - nc; };
 
   // Buffer loads: reads past the end of W (rows >= N) or of A (rows >= M)
-  // return zero in hardware, so no address is clamped and every offset inside
-  // a chunk is an immediate.
+  // return zero in hardware, so no address is clamped.  The row part of every
+  // offset goes in the VGPR offset: the hardware range check covers the VGPR
+  // and instruction offsets, not the scalar one.
   const long long w_rows = max(p.N - n_wave, 0);
   const __amdgpu_buffer_rsrc_t wres = make_rsrc(reinterpret_cast<const T*>(p.w) + (size_t)min(n_wave, p.N) * p.K,
                                                 (unsigned long long)w_rows * p.K * sizeof(T));
@@ -156,7 +157,7 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
     valid = i < nc && kb + c * kLinKC + 8 * (tid & 31) < ke;
     const int off = a_voff + c * kLinKC * (int)sizeof(T);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = buffer_load16(ares, off, i * a_rows8);
+    for (int i = 0; i < 8; ++i) r[i] = buffer_load16(ares, off + i * a_rows8, 0);   // row in the range-checked offset
   };
   auto storeA = [&](const u32x4 (&r)[8], bool valid, int buf) {
 #pragma unroll
