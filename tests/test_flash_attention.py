@@ -128,6 +128,17 @@ def test_key_split_work_groups(dtype, lq, lk, causal):
     check(q, k, v, causal)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("lq,lk,causal", [(600, 600, False), (700, 900, True)])
+def test_key_split_short_tiles(dtype, lq, lk, causal):
+    """Between one and four work-groups per CU (Hq 32) with long rows: two key
+    groups of 32-key tiles per work-group."""
+    q = randn(73, lq, 32, 64, dtype=dtype)
+    k = randn(74, lk, 4, 64, dtype=dtype)
+    v = randn(75, lk, 4, 64, dtype=dtype)
+    check(q, k, v, causal)
+
+
 def test_unequal_lengths_top_left_causal():
     q = randn(40, 40, 8, 64, dtype=torch.float16)
     k = randn(41, 100, 2, 64, dtype=torch.float16)

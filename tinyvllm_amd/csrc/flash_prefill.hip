@@ -866,8 +866,9 @@ int prefill_key_tiles_host(const PrefillParams& p, int qt) {
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
-// head_dim 64 kernel shapes: 0 = 16-row waves, 2 key groups (512 threads);
-// 1 = 16-row waves, 1 key group (256 threads).
+// head_dim 64 kernel shapes (16-row waves): 0 = 2 key groups of 64-key tiles
+// (512 threads); 1 = 1 key group (256 threads); 2 = 2 key groups of 32-key
+// tiles (512 threads).
 template <typename T> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
 #ifdef TV_PREFILL_FIXED
   (void)cfg;
@@ -875,6 +876,7 @@ template <typename T> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp
                      dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
 #else
   if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 2, 64>), grid, dim3(512), 0, stream, pp);
+  else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 2, 32>), grid, dim3(512), 0, stream, pp);
   else hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 1, 64>), grid, dim3(256), 0, stream, pp);
 #endif
 }
@@ -909,13 +911,15 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     }
 #else
     if (d64) {
-      // One work-group per CU or fewer, with rows of 8+ key tiles: two key
-      // groups of 4 waves halve the longest chain (the idle SIMDs would wait
-      // anyway).  Otherwise 4 waves, no split and no merge.  (Measured at
-      // Hq 32: L = 64 / 256 / 512 / 1024 / 2048 take 4.2 / 6.0 / 7.9 / 14.5 /
-      // 35 us; 32-row waves were slower at every length.)
+      // Rows of 8+ key tiles on a grid of fewer than 4 work-groups per CU:
+      // two key groups of 4 waves halve the longest chain; between one and
+      // four per CU also 32-key tiles (smaller registers: 4 waves per SIMD
+      // instead of 2).  Otherwise 4 waves, no split and no merge.  (Measured
+      // at Hq 32: L = 64 / 256 / 512 / 1024 / 2048 take 4.2 / 5.9 / 7.9 / 13.6 /
+      // 35 us; 32-row waves and 4 key groups were slower at every length.)
       const long long wgs = (long long)grid.x * grid.y;
-      const int cfg = (wgs <= 256 && prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8) ? 0 : 1;
+      const bool long_rows = prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8;
+      const int cfg = long_rows && wgs <= 256 ? 0 : (long_rows && wgs < 1024 ? 2 : 1);
       if (dtype == kF16) launch_fa<_Float16>(cfg, grid, pp, stream);
       else launch_fa<__bf16>(cfg, grid, pp, stream);
     } else if (dtype == kF16) {
