@@ -730,33 +730,65 @@ prefill_fa_kernel(const PrefillParams p) {
   }
 }
 
-// Merge the key-chunk partials of query tiles that were split.  grid (Hq, nqt).
+// Merge the key-chunk partials of query tiles that were split.  grid (Hq, nqt),
+// 256 threads: thread (row, quarter) merges 16 output dims of one query row.
+// Chunks are read four at a time with every load of a batch issued together
+// (indexes past the last chunk re-read it and are dropped), so a merge of up to
+// four chunks is one round trip.
 template <int D>
 __global__ void __launch_bounds__(256) prefill_merge_kernel(const PrefillParams p) {
   constexpr int BM = kPrefillBM;
+  constexpr int DQ = D / 4;        // dims per thread
+  constexpr int NV = DQ / 4;       // float4 per thread
   const int h = blockIdx.x;
   const int qt = blockIdx.y;
   const int nchunks = (prefill_key_tiles(p, qt) + p.chunk_tiles - 1) / p.chunk_tiles;
   if (nchunks <= 1) return;
   const int nqt = (p.q_len + BM - 1) / BM;
   const size_t unit0 = ((size_t)h * nqt + qt) * p.max_chunks;
-  for (int idx = threadIdx.x; idx < BM * D; idx += 256) {
-    const int row = idx / D;
-    const int d = idx - row * D;
-    const int qi = qt * BM + row;
-    if (qi >= p.q_len) break;
-    float M = kNegInf;
-    for (int ch = 0; ch < nchunks; ++ch) M = fmaxf(M, p.part_ml[((unit0 + ch) * BM + row) * 2]);
-    const float Mu = M == kNegInf ? 0.0f : M;
-    float num = 0.0f, den = 0.0f;
-    for (int ch = 0; ch < nchunks; ++ch) {
-      const size_t r = (unit0 + ch) * BM + row;
-      const float w = p.part_ml[r * 2 + 1] * fast_exp2(p.part_ml[r * 2] - Mu);
-      num = fmaf(w, p.part_o[r * D + d], num);
-      den += w;
-    }
-    store_as(p.out, (size_t)qi * p.out_stride + (size_t)h * D + d, num / den, p.out_dtype);
+  const int row = threadIdx.x >> 2;
+  const int d0 = (threadIdx.x & 3) * DQ;
+  const int qi = qt * BM + row;
+  if (qi >= p.q_len) return;
+  float M = kNegInf;
+  for (int c0 = 0; c0 < nchunks; c0 += 4) {
+    float mv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mv[u] = p.part_ml[((unit0 + min(c0 + u, nchunks - 1)) * BM + row) * 2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) M = fmaxf(M, mv[u]);
   }
+  const float Mu = M == kNegInf ? 0.0f : M;
+  f32x4 num[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) num[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float den = 0.0f;
+  for (int c0 = 0; c0 < nchunks; c0 += 4) {
+    float2 ml[4];
+    f32x4 o[4][NV];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const size_t r = (unit0 + min(c0 + u, nchunks - 1)) * BM + row;
+      ml[u] = *reinterpret_cast<const float2*>(p.part_ml + r * 2);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) o[u][i] = *reinterpret_cast<const f32x4*>(p.part_o + r * D + d0 + 4 * i);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (c0 + u >= nchunks) break;
+      const float w = ml[u].y * fast_exp2(ml[u].x - Mu);
+      den += w;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) num[i] += o[u][i] * w;
+    }
+  }
+  const float inv = 1.0f / den;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (p.out_dtype == kBF16)
+      store4<__bf16>(p.out, (size_t)qi * p.out_stride + (size_t)h * D + d0 + 4 * i, num[i] * inv, p.out_dtype);
+    else   // f16 or f32 (store4 writes f32 for kF32 whatever T is)
+      store4<_Float16>(p.out, (size_t)qi * p.out_stride + (size_t)h * D + d0 + 4 * i, num[i] * inv, p.out_dtype);
 }
 
 // ---------------------------------------------------------------------------
