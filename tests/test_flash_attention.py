@@ -117,26 +117,35 @@ def test_tinyllama_prefill_config2(length):
     check(q, k, v)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("lq,lk,causal", [(600, 600, False), (520, 520, True), (500, 700, True), (480, 900, False)])
-def test_key_split_work_groups(dtype, lq, lk, causal):
+def test_key_split_work_groups(dtype, lq, lk, causal, d):
     """Grids of at most one work-group per CU with rows of 8+ key tiles run two
-    key groups per work-group and merge them in LDS (head_dim 64)."""
-    q = randn(70, lq, 8, 64, dtype=dtype)
-    k = randn(71, lk, 2, 64, dtype=dtype)
-    v = randn(72, lk, 2, 64, dtype=dtype)
+    key groups per work-group and merge them in LDS."""
+    q = randn(70, lq, 8, d, dtype=dtype)
+    k = randn(71, lk, 2, d, dtype=dtype)
+    v = randn(72, lk, 2, d, dtype=dtype)
     check(q, k, v, causal)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("lq,lk,causal", [(600, 600, False), (700, 900, True)])
-def test_key_split_short_tiles(dtype, lq, lk, causal):
+def test_key_split_short_tiles(dtype, lq, lk, causal, d):
     """Between one and four work-groups per CU (Hq 32) with long rows: two key
     groups of 32-key tiles per work-group."""
-    q = randn(73, lq, 32, 64, dtype=dtype)
-    k = randn(74, lk, 4, 64, dtype=dtype)
-    v = randn(75, lk, 4, 64, dtype=dtype)
+    q = randn(73, lq, 32, d, dtype=dtype)
+    k = randn(74, lk, 4, d, dtype=dtype)
+    v = randn(75, lk, 4, d, dtype=dtype)
     check(q, k, v, causal)
+
+
+@pytest.mark.parametrize("length", [512, 2048])
+def test_llama3_8b_head_prefill(length):
+    """Llama-3-8B head shape (Hq 32, Hkv 8, head_dim 128), fp16, causal."""
+    q, k, v = (randn(80 + i, length, 32 if i == 0 else 8, 128, dtype=torch.float16) for i in range(3))
+    check(q, k, v)
 
 
 def test_unequal_lengths_top_left_causal():

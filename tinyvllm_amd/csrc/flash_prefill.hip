@@ -6,15 +6,15 @@
 // h / (Hq/Hkv).  Every query row keeps key 0, so the reference's -1e9 additive
 // mask and the exclusion used here give the same softmax.
 //
-// Two kernels:
-//  * prefill_mfma_kernel<T, D>: fp16/bf16, D in {64, 128}, Dv == D.  A work-group
-//    of 4 waves owns 64 query rows of one head; each wave owns 16 rows.  Key
-//    tiles of 64 rows are staged in LDS (K row-major, V transposed).  Scores are
-//    computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_{f16,bf16}; the
-//    accumulator layout of S^T (lane = query column, 4 consecutive keys per
-//    16-key block) is exactly the B-operand layout needed for O^T = V^T P^T once
-//    the two operands agree on the order of the reduction index, so P never
-//    leaves registers.
+// Kernels:
+//  * prefill_fa_kernel<T, D, RB, KS, BN>: fp16/bf16, D in {64, 128}, Dv == D.
+//    A work-group owns 64 query rows of one head; KS groups of waves split the
+//    row block's BN-key tiles.  Scores are computed transposed, S^T = K Q^T,
+//    with v_mfma_f32_16x16x32_{f16,bf16}; the accumulator layout of S^T (lane =
+//    query column, 4 consecutive keys per 16-key block) is exactly the
+//    B-operand layout needed for O^T = V^T P^T once the two operands agree on
+//    the order of the reduction index, so P never leaves registers.
+//  * prefill_merge_kernel<D>: merges rows split into key chunks.
 //  * prefill_generic_kernel<T>: any D, Dv <= 256, any element type (fp32 path and
 //    odd head sizes).  One wave per (query row, head); 64 keys per step.
 #include "tv_common.h"
@@ -42,10 +42,7 @@ constexpr int kPrefillBM = 64;   // query rows per work unit (16 per wave)
 #ifndef TV_PREFILL_BN
 #define TV_PREFILL_BN 64
 #endif
-constexpr int kPrefillBN = TV_PREFILL_BN;   // keys per tile (64 or 128)
-#ifndef TV_PREFILL_KSPLIT
-#define TV_PREFILL_KSPLIT 2   // groups of 4 waves splitting a row block's key tiles (head_dim 64)
-#endif
+constexpr int kPrefillBN = TV_PREFILL_BN;   // keys per unit of the chunking and of prefill_key_tiles
 
 // Key tiles query tile qt needs (causal rows stop at the diagonal).
 __device__ __forceinline__ int prefill_key_tiles(const PrefillParams& p, int qt) {
@@ -87,299 +84,8 @@ __device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v, int out_
   }
 }
 
-// KSPLIT groups of 4 waves share the 64 query rows of a work-group; group s
-// takes key tiles kt0 + s, kt0 + s + KSPLIT, ... in its own LDS buffers and the
-// groups merge their (max, row sum, O) through LDS at the end.  Every group
-// runs the same number of steps (idle groups load and skip a clamped tile) so
-// all waves meet at every barrier.
-template <typename T, int D, int KSPLIT>
-__global__ void __launch_bounds__(256 * KSPLIT) prefill_mfma_kernel(const PrefillParams p) {
-  constexpr int BM = kPrefillBM;
-  constexpr int BN = kPrefillBN;
-  constexpr int KP = D + 8;       // LDS pitch of the K tile (elements)
-  constexpr int VP = BN + 4;      // LDS pitch of the V^T tile: 8-byte reads of 16 rows hit distinct banks
-  constexpr int DB = D / 16;      // 16-row blocks of O^T; block DB holds the row sums
-  constexpr int KS = D / 32;      // MFMA steps over the head dim
-  constexpr int VPT = BN * (D / 8) / 256;          // 16-byte K vectors per thread per tile
-  constexpr int VPT2 = (BN / 2) * (D / 8) / 256;   // V key pairs per thread per tile
-  constexpr int SK = BN * KP;                // K tile (elements)
-  constexpr int SV = (D + 16) * VP;          // V^T tile plus 16 rows of ones
-  // V^T tile plus 16 rows of ones: the MFMA against them yields the softmax
-  // row sums of the (rounded) P that the numerator uses, for free.
-  // tile buffers of all groups; reused afterwards for the group merge
-  constexpr int TILE_ELEMS = KSPLIT * (SK + SV);
-  constexpr int MERGE_ELEMS = KSPLIT > 1 ? KSPLIT * (BM * (D + 16) + BM) * 2 : 0;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[TILE_ELEMS > MERGE_ELEMS ? TILE_ELEMS : MERGE_ELEMS];
-
-  const int grp = threadIdx.x >> 8;          // key-split group
-  const int tid = threadIdx.x & 255;         // thread within the group
-  const int wave = tid >> 6;
-  uint16_t* sk = smem + grp * (SK + SV);
-  uint16_t* sv = sk + SK;
-  const int lane = tid & 63;
-  const int g = lane >> 4;        // 0..3
-  const int col = lane & 15;
-
-  const int h = prefill_head(blockIdx.x, p.num_heads, p.xcd_remap);
-  int qt, chunk, nchunks;
-  prefill_unit(p, blockIdx.y, qt, chunk, nchunks);
-  const int kvh = h / (p.num_heads / p.num_kv_heads);
-  const int qi = qt * BM + wave * 16 + col;
-  const int nkt = prefill_key_tiles(p, qt);
-  const int kt0 = chunk * p.chunk_tiles;
-  const int kt1 = min(kt0 + p.chunk_tiles, nkt);
-
-  const T* qg = reinterpret_cast<const T*>(p.q);
-  const T* kg = reinterpret_cast<const T*>(p.k) + (size_t)kvh * D;
-  const T* vg = reinterpret_cast<const T*>(p.v) + (size_t)kvh * D;
-
-  u32x4 qf[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    qf[ks] = qi < p.q_len
-                 ? *reinterpret_cast<const u32x4*>(qg + (size_t)qi * p.q_stride + (size_t)h * D + ks * 32 + g * 8)
-                 : u32x4{0, 0, 0, 0};
-
-  {  // ones rows of the extended V^T (never overwritten by tile stores)
-    const uint16_t one = __builtin_bit_cast(uint16_t, from_float<T>(1.0f));
-    for (int idx = tid; idx < 16 * VP; idx += 256) sv[D * VP + idx] = one;
-  }
-
-  // Per-thread element offsets inside a tile (the tile base is wave-uniform).
-  // K: thread -> (key, 8-dim chunk), consecutive lanes along a row.
-  // V: thread -> (key pair, 8-dim chunk); pairs are interleaved into 32-bit
-  //    words with v_perm so V^T is written with ds_write_b32.
-  int k_row[VPT], k_col[VPT], v_row[VPT2], v_col[VPT2];
-  size_t k_off[VPT], v_off[VPT2];   // element offsets from the tile's first row (full tiles)
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int idx = tid + i * 256;
-    k_row[i] = idx / (D / 8);
-    k_col[i] = idx - k_row[i] * (D / 8);
-    k_off[i] = (size_t)k_row[i] * p.k_stride + k_col[i] * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < VPT2; ++i) {
-    const int unit = tid + i * 256;
-    v_row[i] = 2 * (unit % (BN / 2));
-    v_col[i] = unit / (BN / 2);
-    v_off[i] = (size_t)v_row[i] * p.v_stride + v_col[i] * 8;
-  }
-
-  struct TileRegs {
-    u32x4 k[VPT];
-    u32x4 v[VPT2][2];
-    int k0;   // first key of the tile
-  };
-  // Every step issues the same loads (rows past kv_len re-read the last valid
-  // row), so the compiler waits for exactly the tile it needs; the registers
-  // are not touched until lstore.
-  auto gload = [&](int kt, TileRegs& r) {
-    const int k0 = kt * BN;
-    r.k0 = k0;
-    const T* kb = kg + (size_t)k0 * p.k_stride;
-    const T* vb = vg + (size_t)k0 * p.v_stride;
-    if (k0 + BN <= p.kv_len) {
-#pragma unroll
-      for (int i = 0; i < VPT; ++i) r.k[i] = *reinterpret_cast<const u32x4*>(kb + k_off[i]);
-#pragma unroll
-      for (int i = 0; i < VPT2; ++i) {
-        r.v[i][0] = *reinterpret_cast<const u32x4*>(vb + v_off[i]);
-        r.v[i][1] = *reinterpret_cast<const u32x4*>(vb + v_off[i] + p.v_stride);
-      }
-    } else {
-      const int last = p.kv_len - 1 - k0;
-#pragma unroll
-      for (int i = 0; i < VPT; ++i)
-        r.k[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)min(k_row[i], last) * p.k_stride + k_col[i] * 8);
-#pragma unroll
-      for (int i = 0; i < VPT2; ++i)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          r.v[i][t] = *reinterpret_cast<const u32x4*>(vb + (size_t)min(v_row[i] + t, last) * p.v_stride +
-                                                       v_col[i] * 8);
-    }
-  };
-  auto lstore = [&](const TileRegs& r) {
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) *reinterpret_cast<u32x4*>(&sk[k_row[i] * KP + k_col[i] * 8]) = r.k[i];
-    const bool partial = r.k0 + BN > p.kv_len;   // zero V rows past the sequence
-#pragma unroll
-    for (int i = 0; i < VPT2; ++i) {
-      u32x4 v0 = r.v[i][0], v1 = r.v[i][1];
-      if (partial) {
-        if (r.k0 + v_row[i] >= p.kv_len) v0 = u32x4{0, 0, 0, 0};
-        if (r.k0 + v_row[i] + 1 >= p.kv_len) v1 = u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        uint16_t* dst = &sv[(v_col[i] * 8 + 2 * w) * VP + v_row[i]];
-        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(dst + VP) = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
-      }
-    }
-  };
-
-  f32x4 oacc[DB + 1];
-#pragma unroll
-  for (int i = 0; i <= DB; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = kNegInf;      // running max of the raw scores q.k of this query column
-  const float c = p.scale * kLog2e;
-
-  auto compute = [&](int kt) {
-    const int k0 = kt * BN;
-    // S^T = K Q^T: st[kb][i] = q.k for query qi and key k0 + kb*16 + 4g + i
-    f32x4 st[BN / 16];
-#pragma unroll
-    for (int kb = 0; kb < BN / 16; ++kb) {
-      st[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&sk[(kb * 16 + col) * KP + ks * 32 + g * 8]);
-        st[kb] = mfma16x16x32<T>(a, qf[ks], st[kb]);
-      }
-    }
-    // mask only tiles that cross the diagonal or the end of the sequence
-    if (!(k0 + BN <= p.kv_len && (!p.causal || k0 + BN - 1 <= qt * BM))) {
-      const int lim = p.causal ? min(p.kv_len - 1, qi) : p.kv_len - 1;   // last visible key
-#pragma unroll
-      for (int kb = 0; kb < BN / 16; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st[kb][i] = k0 + kb * 16 + 4 * g + i <= lim ? st[kb][i] : kNegInf;
-    }
-    float mt;
-    {  // max of the 4*BN/16 raw scores with a v_max3 tree
-      float r[BN / 16 * 4];
-#pragma unroll
-      for (int kb = 0; kb < BN / 16; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[kb * 4 + i] = st[kb][i];
-      constexpr int N = BN / 16 * 4;
-      float t[(N + 2) / 3];
-#pragma unroll
-      for (int a = 0; a < N / 3; ++a) t[a] = fmaxf(fmaxf(r[3 * a], r[3 * a + 1]), r[3 * a + 2]);
-      int nt = N / 3;
-      if constexpr (N % 3 == 1) t[nt++] = r[N - 1];
-      if constexpr (N % 3 == 2) t[nt++] = fmaxf(r[N - 2], r[N - 1]);
-      mt = t[0];
-#pragma unroll
-      for (int a = 1; a + 1 < (N + 2) / 3; a += 2) mt = fmaxf(fmaxf(mt, t[a]), t[a + 1]);
-      if constexpr (((N + 2) / 3) % 2 == 0) mt = fmaxf(mt, t[(N + 2) / 3 - 1]);
-    }
-    mt = max_over_g(mt);
-    // the running max is only raised when it grows by more than 8 log2 units
-    // (rare after the first tile); unnormalised weights stay <= 2^8
-    const float mtc = mt * c;
-    float mc = m == kNegInf ? kNegInf : m * c;
-    if (__builtin_amdgcn_ballot_w64(mtc > mc + 8.0f) != 0) {
-      __asm__ volatile("" ::: "memory");
-      const float mn = mtc > mc + 8.0f ? fmaxf(m, mt) : m;
-      const float alpha = mn == kNegInf ? 1.0f : fast_exp2((m - mn) * c);
-      m = mn;
-      mc = m == kNegInf ? kNegInf : m * c;
-#pragma unroll
-      for (int db = 0; db <= DB; ++db) oacc[db] *= alpha;
-    }
-    if (mc == kNegInf) mc = 0.0f;
-    u32x4 pf[BN / 32];
-#pragma unroll
-    for (int kb = 0; kb < BN / 16; ++kb) {
-      const float e0 = fast_exp2(fmaf(st[kb][0], c, -mc));
-      const float e1 = fast_exp2(fmaf(st[kb][1], c, -mc));
-      const float e2 = fast_exp2(fmaf(st[kb][2], c, -mc));
-      const float e3 = fast_exp2(fmaf(st[kb][3], c, -mc));
-      // reduction index kk = 8g + j maps to key 4g+j (j<4) of block 2*ks2 and
-      // key 4g+j-4 (j>=4) of block 2*ks2+1 on both MFMA operands
-      pf[kb >> 1][(kb & 1) * 2] = pack2<T>(e0, e1);
-      pf[kb >> 1][(kb & 1) * 2 + 1] = pack2<T>(e2, e3);
-    }
-    // O^T += V^T P^T (block DB: the ones rows -> row sums)
-#pragma unroll
-    for (int db = 0; db <= DB; ++db) {
-#pragma unroll
-      for (int ks2 = 0; ks2 < BN / 32; ++ks2) {
-        const uint16_t* row = &sv[(db * 16 + col) * VP + ks2 * 32 + 4 * g];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
-        oacc[db] = mfma16x16x32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf[ks2], oacc[db]);
-      }
-    }
-  };
-  // group tile sequence: kt0 + grp + KSPLIT * j, j < nsteps (same count for all groups)
-  const int nsteps = (kt1 - kt0 + KSPLIT - 1) / KSPLIT;
-  auto tile_of = [&](int j) { return min(kt0 + grp + KSPLIT * j, kt1 - 1); };
-  auto step = [&](int j, TileRegs& r) {
-    lds_barrier();
-    lstore(r);
-    lds_barrier();
-    gload(tile_of(j + 2), r);          // two steps ahead (clamped: re-reads are unused)
-    if (kt0 + grp + KSPLIT * j < kt1) compute(kt0 + grp + KSPLIT * j);
-  };
-
-  TileRegs ra, rb;
-  gload(tile_of(0), ra);
-  gload(tile_of(1), rb);
-  // both steps of the loop body are unconditional so the number of loads in
-  // flight is the same on every path (the final odd step is peeled)
-  int j = 0;
-  for (; j + 1 < nsteps; j += 2) {
-    step(j, ra);
-    step(j + 1, rb);
-  }
-  if (j < nsteps) step(j, ra);
-
-  if constexpr (KSPLIT > 1) {
-    // merge the groups: each publishes (scaled max, O unnormalised incl. row sums)
-    lds_barrier();
-    float* so = reinterpret_cast<float*>(smem);                  // [KSPLIT][64 rows][D + 16]
-    float* sm = so + KSPLIT * BM * (D + 16);                     // [KSPLIT][64 rows]
-    const int row = wave * 16 + col;
-#pragma unroll
-    for (int db = 0; db <= DB; ++db)
-      *reinterpret_cast<f32x4*>(&so[(grp * BM + row) * (D + 16) + db * 16 + 4 * g]) = oacc[db];
-    if (g == 0) sm[grp * BM + row] = m == kNegInf ? kNegInf : m * c;
-    lds_barrier();
-    if (grp != 0) return;
-    float M = kNegInf;
-#pragma unroll
-    for (int s2 = 0; s2 < KSPLIT; ++s2) M = fmaxf(M, sm[s2 * BM + row]);
-#pragma unroll
-    for (int db = 0; db <= DB; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s2 = 0; s2 < KSPLIT; ++s2) {
-      const float ms = sm[s2 * BM + row];
-      const float f = ms == kNegInf ? 0.0f : fast_exp2(ms - M);
-#pragma unroll
-      for (int db = 0; db <= DB; ++db)
-        oacc[db] += *reinterpret_cast<const f32x4*>(&so[(s2 * BM + row) * (D + 16) + db * 16 + 4 * g]) * f;
-    }
-    m = M == kNegInf ? kNegInf : M / c;
-  }
-
-  const float lsum = oacc[DB][0];
-  if (qi >= p.q_len) return;
-  const float inv = 1.0f / lsum;
-  if (nchunks == 1) {
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-      store4<T>(p.out, (size_t)qi * p.out_stride + (size_t)h * D + db * 16 + 4 * g, oacc[db] * inv, p.out_dtype);
-    return;
-  }
-  // partial of this key chunk: normalised O plus (max, sum) per query row
-  const int nqt = (p.q_len + BM - 1) / BM;
-  const size_t unit = ((size_t)h * nqt + qt) * p.max_chunks + chunk;
-  const int row = qi - qt * BM;
-  float* po = p.part_o + (unit * BM + row) * D;
-#pragma unroll
-  for (int db = 0; db < DB; ++db) *reinterpret_cast<f32x4*>(po + db * 16 + 4 * g) = oacc[db] * inv;
-  if (g == 0) {
-    p.part_ml[(unit * BM + row) * 2] = m == kNegInf ? kNegInf : m * c;
-    p.part_ml[(unit * BM + row) * 2 + 1] = lsum;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// MFMA kernel, head_dim 64: register-lean softmax, double-buffered tiles
+// MFMA kernel: register-lean softmax, double-buffered tiles
 // ---------------------------------------------------------------------------
 //
 // A work-group owns 64 query rows of one head.  KS groups of QW = 4 / RB waves
@@ -898,18 +604,19 @@ int prefill_key_tiles_host(const PrefillParams& p, int qt) {
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
-// head_dim 64 kernel shapes (16-row waves): 0 = 2 key groups of 64-key tiles
-// (512 threads); 1 = 1 key group (256 threads); 2 = 2 key groups of 32-key
-// tiles (512 threads).
-template <typename T> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
+// Kernel shapes (16-row waves): 0 = 2 key groups (512 threads) of 64-key
+// tiles at head_dim 64, 32-key tiles at 128; 1 = 1 key group (256 threads) of
+// 64-key tiles at head_dim 64, 32-key at 128; 2 = 2 key groups of 32-key tiles.
+template <typename T, int D> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
+  constexpr int BN = D == 64 ? 64 : 32;
 #ifdef TV_PREFILL_FIXED
   (void)cfg;
-  hipLaunchKernelGGL((prefill_fa_kernel<T, 64, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN>), grid,
+  hipLaunchKernelGGL((prefill_fa_kernel<T, D, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN>), grid,
                      dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
 #else
-  if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 2, 64>), grid, dim3(512), 0, stream, pp);
-  else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 2, 32>), grid, dim3(512), 0, stream, pp);
-  else hipLaunchKernelGGL((prefill_fa_kernel<T, 64, 1, 1, 64>), grid, dim3(256), 0, stream, pp);
+  if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, BN>), grid, dim3(512), 0, stream, pp);
+  else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, 32>), grid, dim3(512), 0, stream, pp);
+  else hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 1, BN>), grid, dim3(256), 0, stream, pp);
 #endif
 }
 
@@ -931,35 +638,24 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     }
     const bool d64 = pp.head_dim == 64;
     const dim3 grid(pp.num_heads, units);
-#ifdef TV_PREFILL_V1
-    constexpr int KSP = TV_PREFILL_KSPLIT;
-    const dim3 block(256 * KSP);
+    // Rows of 8+ key tiles on a grid of fewer than 4 work-groups per CU: two
+    // key groups of 4 waves halve the longest chain; between one and four per
+    // CU (head_dim 64) also 32-key tiles (fewer registers: 4 waves per SIMD
+    // instead of 2).  Otherwise 4 waves, no split and no merge.  (Measured at
+    // Hq 32, head_dim 64: L = 64 / 256 / 512 / 1024 / 2048 take 4.2 / 5.9 /
+    // 7.9 / 13.6 / 35 us; 32-row waves and 4 key groups were slower at every
+    // length.  Head_dim 128, Hkv 8, 32-key tiles: L = 512 / 1024 / 2048 take
+    // 11.9 / 24.6 / 62.9 us; two key groups at L = 1024 took 28.6.)
+    const long long wgs = (long long)grid.x * grid.y;
+    const bool long_rows = prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8;
+    const int cfg = long_rows && wgs <= 256 ? 0 : (d64 && long_rows && wgs < 1024 ? 2 : 1);
     if (dtype == kF16) {
-      if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 64, KSP>), grid, block, 0, stream, pp);
-      else hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128, 1>), grid, dim3(256), 0, stream, pp);
+      if (d64) launch_fa<_Float16, 64>(cfg, grid, pp, stream);
+      else launch_fa<_Float16, 128>(cfg, grid, pp, stream);
     } else {
-      if (d64) hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 64, KSP>), grid, block, 0, stream, pp);
-      else hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
+      if (d64) launch_fa<__bf16, 64>(cfg, grid, pp, stream);
+      else launch_fa<__bf16, 128>(cfg, grid, pp, stream);
     }
-#else
-    if (d64) {
-      // Rows of 8+ key tiles on a grid of fewer than 4 work-groups per CU:
-      // two key groups of 4 waves halve the longest chain; between one and
-      // four per CU also 32-key tiles (smaller registers: 4 waves per SIMD
-      // instead of 2).  Otherwise 4 waves, no split and no merge.  (Measured
-      // at Hq 32: L = 64 / 256 / 512 / 1024 / 2048 take 4.2 / 5.9 / 7.9 / 13.6 /
-      // 35 us; 32-row waves and 4 key groups were slower at every length.)
-      const long long wgs = (long long)grid.x * grid.y;
-      const bool long_rows = prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8;
-      const int cfg = long_rows && wgs <= 256 ? 0 : (long_rows && wgs < 1024 ? 2 : 1);
-      if (dtype == kF16) launch_fa<_Float16>(cfg, grid, pp, stream);
-      else launch_fa<__bf16>(cfg, grid, pp, stream);
-    } else if (dtype == kF16) {
-      hipLaunchKernelGGL((prefill_mfma_kernel<_Float16, 128, 1>), grid, dim3(256), 0, stream, pp);
-    } else {
-      hipLaunchKernelGGL((prefill_mfma_kernel<__bf16, 128, 1>), grid, dim3(256), 0, stream, pp);
-    }
-#endif
     if (max_chunks > 1) {
       const dim3 mgrid(pp.num_heads, (pp.q_len + kPrefillBM - 1) / kPrefillBM);
       if (d64) hipLaunchKernelGGL((prefill_merge_kernel<64>), mgrid, dim3(256), 0, stream, pp);
