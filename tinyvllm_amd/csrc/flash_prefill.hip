@@ -89,9 +89,9 @@ __device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v, int out_
 // ---------------------------------------------------------------------------
 //
 // A work-group owns 64 query rows of one head.  KS groups of QW = 4 / RB waves
-// split the row block's key tiles (group s takes tiles kt0 + s + KS j); every
-// wave owns RB blocks of 16 query rows, so each K / V fragment read from LDS
-// feeds RB matrix products.  Per 64-key tile a wave computes S^T = K Q^T with
+// split the row block's BN-key tiles (group s takes tiles s + KS j of its key
+// range); every wave owns RB blocks of 16 query rows, so each K / V fragment
+// read from LDS feeds RB matrix products.  Per tile a wave computes S^T = K Q^T with
 // Q pre-scaled by scale * log2(e) and the accumulator initialised to -m (the
 // running reference maximum of the query), so the scores come out of the
 // matrix cores already in the log2 domain relative to m and go straight into
