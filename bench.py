@@ -37,10 +37,11 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
-# HBM bytes per launch of the primary decode kernel measured with two rocprofv3
-# --pmc passes (FETCH_SIZE x2.000 + WRITE_SIZE x1.000, factors from a plain
-# 1 GiB copy), recorded in profiles/paged_decode_llama3_8b_f16.md.
-PRIMARY_TRAFFIC_BYTES = 2501465088
+# HBM bytes per launch of the primary decode (longest-first order kernel +
+# decode kernel) measured with two rocprofv3 --pmc passes (FETCH_SIZE x1.99994 +
+# WRITE_SIZE x1.000, factors from a plain 1 GiB copy), recorded in
+# profiles/paged_decode_llama3_8b_f16.md.
+PRIMARY_TRAFFIC_BYTES = 2501426441
 PRIMARY_TRAFFIC_SOURCE = "profiles/paged_decode_llama3_8b_f16.md"
 
 
@@ -145,6 +146,14 @@ def bench_prefill(steps, warmup):
     wms = timed(write, steps, warmup, graph=True)
     tot = sum(per)
     flops = wl.flops()
+    # Llama-3-8B heads (Hq 32 / Hkv 8, head_dim 128), one 2048-token prompt.
+    g = torch.Generator(device="cuda").manual_seed(0)
+    L8, hq8, hkv8, d8 = 2048, 32, 8, 128
+    q8 = torch.randn((1, L8, hq8, d8), generator=g, device="cuda").half()
+    k8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
+    v8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
+    ms8 = timed(PrefillPlan(q8, k8, v8, True).run, steps, warmup, graph=True)
+    flops8 = 2 * hq8 * d8 * L8 * (L8 + 1)
     return {
         "workload": "prefill_tinyllama_f16_L512+L1024 (Hq32 Hkv4 D64, causal) + fused KV write",
         "value": round(flops / (tot * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
@@ -153,6 +162,10 @@ def bench_prefill(steps, warmup):
         "frac_of_fp16_mfma_peak": round(flops / (tot * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
         "kv_write_ms": round(wms, 5),
         "kv_write_gbs": round(wl.kv_write_bytes() / (wms * 1e-3) / 1e9, 1),
+        "llama3_8b_heads_f16_L2048": {
+            "value": round(flops8 / (ms8 * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+            "ms": round(ms8, 5), "flops": flops8,
+            "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)},
     }
 
 
