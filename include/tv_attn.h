@@ -50,8 +50,8 @@ const char* tv_last_error(void);
  * Workspace (bytes) needed by tv_paged_decode for the split-context partials:
  * num_seqs * num_heads * ceil(max_blocks*block_size / partition_size)
  * * (head_dim + 2) floats.  When every sequence fits one partition and
- * 32 <= num_seqs <= 1024 it is num_seqs ints (rounded up to 256 bytes) for a
- * longest-first schedule of the sequences, which tv_paged_decode uses when
+ * 32 <= num_seqs <= 1024 it is num_seqs + 1 ints (rounded up to 256 bytes) for
+ * a longest-first schedule of the sequences, which tv_paged_decode uses when
  * the caller provides it and skips otherwise; else 0.  Host-only computation.
  */
 size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,

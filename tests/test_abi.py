@@ -57,7 +57,9 @@ def test_workspace_size_is_host_arithmetic():
     assert lib.tv_flash_prefill_workspace_bytes(1024, 1024, 32, 64, 64, 1, 1, 0) == 0      # default: no split
     assert lib.tv_flash_prefill_workspace_bytes(1024, 1024, 32, 64, 64, 1, 0, 4) == 0      # fp32: generic kernel
     assert lib.tv_paged_decode_workspace_bytes(4, 32, 64, 16, 16, 512) == 0      # one partition
-    assert lib.tv_paged_decode_workspace_bytes(256, 32, 128, 256, 16, 4096) == 1024   # schedule only
+    # one partition: the schedule (KV heads per row + order) only, in 256-byte units
+    assert lib.tv_paged_decode_workspace_bytes(256, 32, 128, 256, 16, 4096) == 1280
+    assert lib.tv_paged_decode_workspace_bytes(255, 32, 128, 256, 16, 4096) == 1024
     assert lib.tv_paged_decode_workspace_bytes(300, 32, 128, 256, 16, 4096) == 1280
     # 256 seqs x 32 heads x 8 partitions x (128 + 2) floats
     assert lib.tv_paged_decode_workspace_bytes(256, 32, 128, 256, 16, 512) == 256 * 32 * 8 * 130 * 4

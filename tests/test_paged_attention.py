@@ -169,6 +169,35 @@ def test_large_batch_runs_longest_first(dtype):
     check((q, kc, vc, bt, cl), 16, 4, 128, 16, dtype, partition_size=4096)
 
 
+@pytest.mark.parametrize("spread", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_scheduled_launch_many_sequences(spread, dtype):
+    """256 sequences x 8 KV heads in one partition: the scheduled launch, with
+    KV head pairs per work-group when the lengths are spread (longest >= 3x
+    shortest) and single heads when they are alike; also a context of 0 and
+    one beyond the table."""
+    rng = np.random.Generator(np.random.PCG64(21))
+    ctx = rng.integers(1, 200, 256) if spread else rng.integers(150, 200, 256)
+    ctx = ctx.astype(np.int32)
+    if spread:
+        ctx[7] = 0
+    case = build_case(22, ctx.tolist(), 32, 8, 128, 16, dtype, width=13)
+    q, kc, vc, bt, cl = case
+    cl = cl.copy()
+    cl[40] = 100000
+    check((q, kc, vc, bt, cl), 32, 8, 128, 16, dtype)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 4, 64), (16, 2, 128), (24, 6, 64)])
+def test_scheduled_launch_group_shapes(hq, hkv, d):
+    """Scheduled launches over several GQA shapes (Hkv / 2 pairs per sequence
+    when the item count and the length spread allow it)."""
+    rng = np.random.Generator(np.random.PCG64(23))
+    ctx = rng.integers(1, 120, 900).astype(np.int32)
+    case = build_case(24, ctx.tolist(), hq, hkv, d, 16, torch.float16, width=8)
+    check(case, hq, hkv, d, 16, torch.float16)
+
+
 def test_deterministic():
     case = build_case(11, [100, 700, 3], 32, 8, 128, 16, torch.float16)
     a = run(*case, 32, 8, 128, 16, partition_size=128)

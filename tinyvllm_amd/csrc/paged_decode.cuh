@@ -2,10 +2,15 @@
 // block-paged K/V cache [num_blocks, block_size, Hkv, D].
 //
 // Work decomposition
-//   grid.x = context partition, grid.y = (KV head, query-head chunk), grid.z = sequence.
-//   A work-group of NW waves handles one KV head for GT query heads of its GQA
-//   group, so every K/V row fetched from HBM is used by GT query heads.
-//   Waves take interleaved tiles of TT tokens inside the partition.
+//   grid.x = context partition, grid.y = (KV head, query-head chunk), grid.z =
+//   sequence.  A work-group of NW waves handles one KV head -- or, in a
+//   scheduled launch with head pairs, two adjacent KV heads -- each for GT
+//   query heads of its GQA group, so
+//   every K/V row fetched from HBM is used by GT query heads.  With hpw heads
+//   per work-group wave w serves head w % hpw; the NW / hpw waves of a head
+//   take interleaved tiles of TT tokens inside the partition, and the waves of
+//   the hpw heads read the same tokens together (hpw * D contiguous elements of
+//   each cache row [token, Hkv, D]).
 //
 // Lane layout inside a wave
 //   A cache row (one token, one KV head) is D*sizeof(T) bytes.  LPR lanes cover
@@ -47,9 +52,6 @@
 #ifndef TV_DECODE_BT_PREFETCH
 #define TV_DECODE_BT_PREFETCH 0  // look the next tile's block id up one tile ahead
 #endif
-#ifndef TV_DECODE_PREFETCH
-#define TV_DECODE_PREFETCH 0     // register double-buffering of the next tile
-#endif
 
 namespace tv {
 
@@ -74,7 +76,8 @@ struct DecodeParams {
   int partition_size;        // tokens per work-group
   int max_parts;             // ceil(max_blocks*block_size / partition_size)
   int out_dtype;
-  const int* order;          // [B] sequence of work-group row z (longest first), or null: z
+  const int* sched;          // scheduled launch: [0] KV heads per row, [1..B] longest-first order
+  int num_seqs;
 };
 
 __device__ __forceinline__ int decode_len(const DecodeParams& p, int b, float& bias) {
@@ -118,6 +121,20 @@ __device__ __forceinline__ u32x4 load_row16(const void* ptr) {
 #endif
 }
 
+__device__ __forceinline__ u32x4 buffer_load_nt16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, TV_DECODE_NT ? 2 : 0));
+}
+
+// Whether every TT-token tile of a launch lies in one cache block (one
+// wave-uniform table lookup per tile, buffer loads from the tile's first row).
+template <typename T, int D, int GT>
+inline bool decode_uniform_tiles(int block_size, int partition_size, int num_kv_heads) {
+  constexpr int TT = DecodeShape<T, D, GT>::TT;
+  const bool pow2 = block_size > 0 && (block_size & (block_size - 1)) == 0;
+  return pow2 && block_size % TT == 0 && partition_size % TT == 0 &&
+         (long long)TT * num_kv_heads * D * (long long)sizeof(T) < (1LL << 31);
+}
+
 // Running maxima are only raised when a tile's maximum exceeds them by more
 // than this many log2 units, so most tiles skip the rescale of l and acc; the
 // unnormalised weights stay <= 2^kRescaleSlack, far from fp32 overflow.
@@ -151,40 +168,69 @@ __device__ __forceinline__ float swizzle_xor16(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
 }
 
-template <typename T, int D, int GT, int NW>
-__global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_kernel(const DecodeParams p) {
+// Shared memory of one decode work-group: per wave and 32-lane half the
+// unnormalised accumulators and sums of its GT query heads, per wave the maxima.
+template <int D, int GT, int NW>
+struct DecodeSmem {
+  float acc[NW][2][GT][D];
+  float l[NW][2][GT];
+  float m[NW][GT];
+};
+
+// Where one pass over a token range leaves its result: the final output
+// out[b, h, :], or a partial -- output normalised by its own sum, running
+// maximum (log2 units) and sum -- at slot slot0 + (h - first query head of the
+// work-group) * slot_step of part_o [*, D] / part_ml [*, 2].
+struct DecodeDest {
+  bool final_out;
+  size_t slot0;
+  int slot_step;
+};
+
+// First query head served by work-group row ky with hpw KV heads per work-group.
+template <int GT>
+__device__ __forceinline__ int decode_first_head(const DecodeParams& p, int ky, int hpw) {
+  const int group = p.num_heads / p.num_kv_heads;
+  return (ky / p.head_chunks) * hpw * group + (ky % p.head_chunks) * GT;
+}
+
+// Attention of work-group row ky's query heads over tokens [start, end) of
+// sequence b (start < end), with hpw (1, or HPW when HPW > 1) KV heads per
+// work-group.  Wave w serves KV head (ky / head_chunks) * hpw + w % hpw with
+// the GT query heads (ky % head_chunks) * GT .. of its GQA group;
+// bias is the reference's additive mask term (-1e9 when context_len <= 0).
+// Ends with the merged result written to dst.  Uses sm from its merge step on:
+// a caller that runs several ranges in one work-group separates them with a
+// barrier.
+template <typename T, int D, int GT, int NW, int HPW, bool UB>
+__device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D, GT, NW>& sm, int b, int ky,
+                                             int hpw_in, int start, int end, float bias,
+                                             const DecodeDest& dst) {
   using S = DecodeShape<T, D, GT>;
   constexpr int LPR = S::LPR, VPL = S::VPL, RPI = S::RPI, NR = S::NR, TT = S::TT;
   constexpr int EPV = S::EPV, EPL = S::EPL;
-
-  __shared__ float sh_acc[NW][2][GT][D];   // per wave, per 32-lane half
-  __shared__ float sh_l[NW][2][GT];
-  __shared__ float sh_m[NW][GT];
+  static_assert(HPW == 1 || HPW == 2, "one or two KV heads per work-group");
+  const int hpw = HPW == 1 ? 1 : hpw_in;
+  const int wph = NW / hpw;       // waves per KV head
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r = lane / LPR;
   const int c = lane % LPR;
-  const int part = blockIdx.x;
-  const int b = p.order ? p.order[blockIdx.z] : (int)blockIdx.z;
-  const int kh = blockIdx.y / p.head_chunks;
+  const int hw = wave & (hpw - 1);   // head of this work-group served by the wave
+  const int wi = wave / hpw;         // the wave's index among that head's waves
+  const int kh = (ky / p.head_chunks) * hpw + hw;
   const int group = p.num_heads / p.num_kv_heads;
-  const int h0 = kh * group + (blockIdx.y % p.head_chunks) * GT;
-
-  float bias;
-  const int len = decode_len(p, b, bias);
-  const int nparts = (len + p.partition_size - 1) / p.partition_size;
-  if (part >= nparts) return;
-  const int start = part * p.partition_size;
-  const int end = min(start + p.partition_size, len);
+  const int hfirst = decode_first_head<GT>(p, ky, hpw);
+  const int h0 = hfirst + hw * group;   // first query head of this wave
 
   const T* qp = reinterpret_cast<const T*>(p.q) + ((size_t)b * p.num_heads + h0) * D;
   const T* kc = reinterpret_cast<const T*>(p.k_cache) + (size_t)kh * D;
   const T* vc = reinterpret_cast<const T*>(p.v_cache) + (size_t)kh * D;
   const int* bt = p.block_tables + (size_t)b * p.bt_stride;
   const size_t row_stride = (size_t)p.num_kv_heads * D;          // elements between cache rows
-  const bool uniform_block = p.block_size % TT == 0 && p.partition_size % TT == 0 && p.bs_log2 >= 0;
+  const int lane_off = (int)((r * row_stride + c * EPV) * sizeof(T));   // bytes from a tile's first row
 
   u32x4 qv[GT][VPL];
 #pragma unroll
@@ -207,41 +253,30 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
 
   // Fetch the K/V rows of the tile starting at token t0 (rows past `end` or in
   // an invalid block are zero and marked invalid).
-  constexpr bool kBtAhead = TV_DECODE_BT_PREFETCH && !TV_DECODE_PREFETCH;
+  constexpr bool kBtAhead = TV_DECODE_BT_PREFETCH;
   auto fetch = [&](int t0, int blk_ahead, u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR]) {
-    if (uniform_block) {
-      // the whole tile lies in one cache block: one wave-uniform table lookup
+    if constexpr (UB) {
+      // The whole tile lies in one cache block: one wave-uniform table lookup,
+      // then buffer loads from the tile's first row.  The buffer's range ends
+      // at the last attended row of the tile (nothing when the block id is
+      // invalid), so rows past it read as zero without per-row branches, and
+      // the lane offsets are the same for every tile.
       const int blk = kBtAhead ? blk_ahead : bt[t0 >> p.bs_log2];
       const bool blk_ok = (unsigned)blk < (unsigned)p.num_blocks;
       bad |= !blk_ok;
-      const size_t base = ((size_t)blk * p.block_size + (t0 & (p.block_size - 1)) + r) * row_stride;
-      if (blk_ok && t0 + TT <= end) {
-        // full tile: no per-row predication
+      const int rows = blk_ok ? min(TT, end - t0) : 0;
+      const size_t row0 = (size_t)(blk_ok ? blk : 0) * p.block_size + (t0 & (p.block_size - 1));
+      const unsigned long long nrec = (unsigned long long)rows * row_stride * sizeof(T);
+      const auto kres = make_rsrc(kc + row0 * row_stride, nrec);
+      const auto vres = make_rsrc(vc + row0 * row_stride, nrec);
 #pragma unroll
-        for (int j = 0; j < NR; ++j) {
-          valid[j] = true;
+      for (int j = 0; j < NR; ++j) {
+        valid[j] = j * RPI + r < rows;
+        const int off = lane_off + j * RPI * (int)(row_stride * sizeof(T));
 #pragma unroll
-          for (int v = 0; v < VPL; ++v) {
-            const size_t off = base + (size_t)j * RPI * row_stride + (v * LPR + c) * EPV;
-            kr[j][v] = load_row16(kc + off);
-            vr[j][v] = load_row16(vc + off);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < NR; ++j) {
-          valid[j] = blk_ok && (t0 + j * RPI + r < end);
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) {
-            const size_t off = base + (size_t)j * RPI * row_stride + (v * LPR + c) * EPV;
-            if (valid[j]) {
-              kr[j][v] = load_row16(kc + off);
-              vr[j][v] = load_row16(vc + off);
-            } else {
-              kr[j][v] = u32x4{0, 0, 0, 0};
-              vr[j][v] = u32x4{0, 0, 0, 0};
-            }
-          }
+        for (int v = 0; v < VPL; ++v) {
+          kr[j][v] = buffer_load_nt16(kres, off + v * LPR * 16, 0);
+          vr[j][v] = buffer_load_nt16(vres, off + v * LPR * 16, 0);
         }
       }
     } else {
@@ -287,12 +322,13 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
         float d = 0.0f;
 #pragma unroll
         for (int v = 0; v < VPL; ++v) {
+          const u32x4 qg = qv[g][v];
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             if constexpr (sizeof(T) == 4) {
-              d = fmaf(u32_as_f32(qv[g][v][w]), u32_as_f32(kr[j][v][w]), d);
+              d = fmaf(u32_as_f32(qg[w]), u32_as_f32(kr[j][v][w]), d);
             } else {
-              d = dot2<T>(qv[g][v][w], kr[j][v][w], d);
+              d = dot2<T>(qg[w], kr[j][v][w], d);
             }
           }
         }
@@ -363,35 +399,16 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
     }
   };
 
-#if TV_DECODE_PREFETCH
-  {
-    u32x4 ka[NR][VPL], va[NR][VPL], kb[NR][VPL], vb[NR][VPL];
-    bool oka[NR], okb[NR];
-    int t0 = start + wave * TT;
-    if (t0 < end) fetch(t0, 0, ka, va, oka);
-    while (t0 < end) {
-      const int t1 = t0 + NW * TT;
-      if (t1 < end) fetch(t1, 0, kb, vb, okb);
-      consume(ka, va, oka);
-      if (t1 >= end) break;
-      const int t2 = t1 + NW * TT;
-      if (t2 < end) fetch(t2, 0, ka, va, oka);
-      consume(kb, vb, okb);
-      t0 = t2;
-    }
-  }
-#else
   int blk_next = 0;
-  if (kBtAhead && uniform_block && start + wave * TT < end) blk_next = bt[(start + wave * TT) >> p.bs_log2];
-  for (int t0 = start + wave * TT; t0 < end; t0 += NW * TT) {
+  if (kBtAhead && UB && start + wi * TT < end) blk_next = bt[(start + wi * TT) >> p.bs_log2];
+  for (int t0 = start + wi * TT; t0 < end; t0 += wph * TT) {
     u32x4 kr[NR][VPL], vr[NR][VPL];
     bool valid[NR];
     const int blk_cur = blk_next;
-    if (kBtAhead && uniform_block && t0 + NW * TT < end) blk_next = bt[(t0 + NW * TT) >> p.bs_log2];
+    if (kBtAhead && UB && t0 + wph * TT < end) blk_next = bt[(t0 + wph * TT) >> p.bs_log2];
     fetch(t0, blk_cur, kr, vr, valid);
     consume(kr, vr, valid);
   }
-#endif
 
   // ---- merge row groups and waves ------------------------------------------
   // 1) common maximum per head across the wave; rescale each group onto it
@@ -426,36 +443,40 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) sh_acc[wave][half][g][(v * LPR + c) * EPV + e] = acc[g][v * EPV + e];
+        for (int e = 0; e < EPV; ++e) sm.acc[wave][half][g][(v * LPR + c) * EPV + e] = acc[g][v * EPV + e];
       if (c == 0) {
-        sh_l[wave][half][g] = l[g];
-        if (half == 0) sh_m[wave][g] = m[g];
+        sm.l[wave][half][g] = l[g];
+        if (half == 0) sm.m[wave][g] = m[g];
       }
     }
   }
   const bool any_bad = __syncthreads_or(bad ? 1 : 0) != 0;
 
   const int hq = p.num_heads;
-  for (int idx = tid; idx < GT * D; idx += 64 * NW) {
-    const int g = idx / D;
-    const int d = idx - g * D;
+  for (int idx = tid; idx < hpw * GT * D; idx += 64 * NW) {
+    const int oh = idx / (GT * D);      // head of the work-group; its waves are oh, oh + hpw, ...
+    const int g = (idx / D) % GT;
+    const int d = idx % D;
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, sh_m[w][g]);
+    for (int k = 0; k < NW; ++k)
+      if (k < wph) M = fmaxf(M, sm.m[oh + k * hpw][g]);
     const float Mu = M == kNegInf ? 0.0f : M;
     float L = 0.0f, O = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = fast_exp2(sh_m[w][g] - Mu);
-      L += (sh_l[w][0][g] + sh_l[w][1][g]) * f;
-      O += (sh_acc[w][0][g][d] + sh_acc[w][1][g][d]) * f;
+    for (int k = 0; k < NW; ++k) {
+      if (k >= wph) break;
+      const int w = oh + k * hpw;
+      const float f = fast_exp2(sm.m[w][g] - Mu);
+      L += (sm.l[w][0][g] + sm.l[w][1][g]) * f;
+      O += (sm.acc[w][0][g][d] + sm.acc[w][1][g][d]) * f;
     }
-    const int h = h0 + g;
-    if (nparts == 1) {
+    const int h = hfirst + oh * group + g;
+    if (dst.final_out) {
       const float val = any_bad ? __builtin_nanf("") : O / L;
       store_as(p.out, ((size_t)b * hq + h) * D + d, val, p.out_dtype);
     } else {
-      const size_t slot = ((size_t)b * hq + h) * p.max_parts + part;
+      const size_t slot = dst.slot0 + (size_t)(h - hfirst) * dst.slot_step;
       p.part_o[slot * D + d] = O / L;
       if (d == 0) {
         p.part_ml[slot * 2] = any_bad ? __builtin_nanf("") : M;
@@ -465,12 +486,56 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
   }
 }
 
+
+// One work-group per (partition, KV head x query-head chunk, sequence).
+template <typename T, int D, int GT, int NW, bool UB>
+__global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_kernel(const DecodeParams p) {
+  __shared__ DecodeSmem<D, GT, NW> sm;
+  const int part = blockIdx.x;
+  const int b = blockIdx.z;
+  float bias;
+  const int len = decode_len(p, b, bias);
+  const int nparts = (len + p.partition_size - 1) / p.partition_size;
+  if (part >= nparts) return;
+  const int start = part * p.partition_size;
+  const int end = min(start + p.partition_size, len);
+  const int ky = blockIdx.y;
+  const DecodeDest dst{nparts == 1, ((size_t)b * p.num_heads + decode_first_head<GT>(p, ky, 1)) * p.max_parts + part,
+                       p.max_parts};
+  decode_range<T, D, GT, NW, 1, UB>(p, sm, b, ky, 1, start, end, bias, dst);
+}
+
+// Scheduled launch of whole sequences: work-group i of a 1-D grid takes item i
+// -- (sequence, row) with the sequences in the longest-first order of
+// decode_order_kernel and hpw KV heads per row.  Work-groups are dispatched in
+// index order (dealt round-robin to the XCDs), so the items start longest
+// first.  The grid has one work-group per item at hpw = 1; with head pairs the
+// upper half, dispatched last, has no item and exits.
+template <typename T, int D, int GT, int NW, int HPW, bool UB>
+__global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_scheduled_kernel(const DecodeParams p) {
+  __shared__ DecodeSmem<D, GT, NW> sm;
+  const int hpw = HPW > 1 ? p.sched[0] : 1;
+  const int rows = p.num_kv_heads / hpw * p.head_chunks;
+  const int item = blockIdx.x;
+  if (item >= p.num_seqs * rows) return;
+  const int b = p.sched[1 + item / rows];
+  float bias;
+  const int len = decode_len(p, b, bias);
+  const DecodeDest dst{true, 0, 0};
+  decode_range<T, D, GT, NW, HPW, UB>(p, sm, b, item % rows, hpw, 0, len, bias, dst);
+}
+
 // Merge the partition partials of each (sequence, query head).  Launched with
 // grid (Hq, B) and 64 threads; sequences that fit one partition were written by
 // the main kernel and are skipped here.
 __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodeParams p, int head_dim);
+
+#ifndef TV_DECODE_PAIR_SPREAD
+#define TV_DECODE_PAIR_SPREAD 3
+#endif
+constexpr int kDecodePairSpread = TV_DECODE_PAIR_SPREAD;
 __global__ void __launch_bounds__(1024) decode_order_kernel(const int* context_lens, int num_seqs, int width,
-                                                            int* order);
+                                                            int pair_ok, int* sched);
 
 
 }  // namespace tv

@@ -12,16 +12,74 @@ namespace tv {
 #endif
 constexpr int kDecodeWaves = TV_DECODE_WAVES;   // waves per work-group
 
-// Launch the main kernel for element type T.  Returns false when (D, GT) has no
+// Work-groups of the paired scheduled kernel resident at once on the current
+// device (occupancy x CUs), queried once per device and instantiation.
+template <typename T, int D, int GT, bool UB>
+int scheduled_pair_slots() {
+  static int cache[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cache[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, paged_decode_scheduled_kernel<T, D, GT, kDecodeWaves, 2, UB>, 64 * kDecodeWaves, 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    cache[dev] = per_cu * cus;
+  }
+  return cache[dev];
+}
+
+// Whether a scheduled launch may pair KV heads: Hkv even and at least 5/4
+// paired items per resident work-group, so that the longest-first order still
+// has short items left to fill the end of the launch (with fewer, pairing
+// only idles CUs).  The length spread is checked on the device.
+template <typename T, int D, int GT>
+bool decode_pair_allowed(const DecodeParams& p) {
+  if (p.num_kv_heads % 2 != 0) return false;
+  const bool ub = decode_uniform_tiles<T, D, GT>(p.block_size, p.partition_size, p.num_kv_heads);
+  const int slots = ub ? scheduled_pair_slots<T, D, GT, true>() : scheduled_pair_slots<T, D, GT, false>();
+  const long long items = (long long)p.num_seqs * (p.num_kv_heads / 2) * p.head_chunks;
+  return 4 * items >= 5LL * slots;
+}
+
+template <typename T>
+bool decode_pair_allowed(const DecodeParams& p, int head_dim, int gt);
+
+// Launch the decode kernel for element type T: the scheduled kernel when p.sched
+// is set (pair: Hkv is even, so rows may take two KV heads; grid B x Hkv x
+// head chunks, checked against 2^31 by the caller), else the partitioned
+// kernel on `grid`.  Returns false when (D, GT) has no
 // instantiation.
 template <typename T>
-bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, dim3 grid, hipStream_t stream);
+bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, bool pair, dim3 grid, hipStream_t stream);
 
-#define TV_DECODE_CASE(T, D, GT)                                                      \
-  if (head_dim == D && gt == GT) {                                                    \
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, GT, kDecodeWaves>), grid,           \
-                       dim3(64 * kDecodeWaves), 0, stream, p);                        \
-    return true;                                                                      \
+#define TV_DECODE_SCHEDULED(T, D, GT, HPW, UB)                                                    \
+  {                                                                                               \
+    hipLaunchKernelGGL((paged_decode_scheduled_kernel<T, D, GT, kDecodeWaves, HPW, UB>),          \
+                       dim3(p.num_seqs * p.num_kv_heads * p.head_chunks), dim3(64 * kDecodeWaves), \
+                       0, stream, p);                                                             \
+    return true;                                                                                  \
+  }
+
+#define TV_DECODE_CASE(T, D, GT)                                                                  \
+  if (head_dim == D && gt == GT) {                                                                \
+    const bool ub = decode_uniform_tiles<T, D, GT>(p.block_size, p.partition_size, p.num_kv_heads); \
+    if (p.sched) {                                                                                \
+      if (pair && ub) TV_DECODE_SCHEDULED(T, D, GT, 2, true)                                         \
+      if (pair) TV_DECODE_SCHEDULED(T, D, GT, 2, false)                                              \
+      if (ub) TV_DECODE_SCHEDULED(T, D, GT, 1, true)                                                 \
+      TV_DECODE_SCHEDULED(T, D, GT, 1, false)                                                        \
+    }                                                                                             \
+    if (ub)                                                                                       \
+      hipLaunchKernelGGL((paged_decode_kernel<T, D, GT, kDecodeWaves, true>), grid,               \
+                         dim3(64 * kDecodeWaves), 0, stream, p);                                  \
+    else                                                                                          \
+      hipLaunchKernelGGL((paged_decode_kernel<T, D, GT, kDecodeWaves, false>), grid,              \
+                         dim3(64 * kDecodeWaves), 0, stream, p);                                  \
+    return true;                                                                                  \
   }
 
 #define TV_DECODE_ALL_GT(T, D) \
@@ -30,9 +88,26 @@ bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, dim3 grid,
   TV_DECODE_CASE(T, D, 4)      \
   TV_DECODE_CASE(T, D, 8)
 
+#define TV_DECODE_PAIR_CASE(T, D, GT) \
+  if (head_dim == D && gt == GT) return decode_pair_allowed<T, D, GT>(p);
+#define TV_DECODE_PAIR_ALL_GT(T, D) \
+  TV_DECODE_PAIR_CASE(T, D, 1)      \
+  TV_DECODE_PAIR_CASE(T, D, 2)      \
+  TV_DECODE_PAIR_CASE(T, D, 4)      \
+  TV_DECODE_PAIR_CASE(T, D, 8)
+
 #define TV_DECODE_DEFINE(T)                                                                      \
   template <>                                                                                    \
-  bool launch_paged_decode<T>(const DecodeParams& p, int head_dim, int gt, dim3 grid,            \
+  bool decode_pair_allowed<T>(const DecodeParams& p, int head_dim, int gt) {                     \
+    TV_DECODE_PAIR_ALL_GT(T, 16)                                                                 \
+    TV_DECODE_PAIR_ALL_GT(T, 32)                                                                 \
+    TV_DECODE_PAIR_ALL_GT(T, 64)                                                                 \
+    TV_DECODE_PAIR_ALL_GT(T, 128)                                                                \
+    TV_DECODE_PAIR_ALL_GT(T, 256)                                                                \
+    return false;                                                                                \
+  }                                                                                              \
+  template <>                                                                                    \
+  bool launch_paged_decode<T>(const DecodeParams& p, int head_dim, int gt, bool pair, dim3 grid, \
                               hipStream_t stream) {                                              \
     TV_DECODE_ALL_GT(T, 16)                                                                      \
     TV_DECODE_ALL_GT(T, 32)                                                                      \

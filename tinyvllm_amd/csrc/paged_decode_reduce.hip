@@ -66,24 +66,35 @@ __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodePar
   }
 }
 
-// Longest-first schedule of an unsplit decode launch: order[rank] = b.
-// Sequences are ranked by 16 length classes (attended length * 16 / (width + 1)),
-// longest class first, batch order inside a class -- one ballot per class and
-// wave instead of a full sort.  Work-groups are dispatched in grid order, so
-// the longest sequences start first and the last ones to start are short: the
-// launch does not end on a few long sequences streaming while most CUs idle.
-// Any permutation is correct; this one only shortens the tail.  One
+// Schedule of an unsplit launch for paged_decode_scheduled_kernel: sched[0] =
+// KV heads per row, sched[1 + rank] = b.  Sequences are ranked by 16 length classes (attended
+// length * 16 / (width + 1)), longest class first, batch order inside a class
+// -- one ballot per class and wave instead of a full sort.  Work-groups are
+// dispatched in grid order, so the longest sequences start first and the last
+// ones to start are short: the launch does not end on a few long sequences
+// streaming while most CUs idle.  Any permutation is correct; this one only
+// shortens the tail.
+// sched[0] = KV heads per row: 2 when pairing is allowed (pair_ok, decided on
+// the host from the item count) and the lengths are spread (longest >=
+// kDecodePairSpread * shortest), else 1.  Pairs read each cache row's two
+// heads together, but halve the number of items and double their length;
+// that pays when the longest-first order can fill the end of the launch with
+// short sequences, and loses when lengths are alike (on MI355X, 256
+// Llama-3-8B-head sequences: 384 vs 401 us for U[512, 4096] lengths, 442 vs
+// 418 us for equal lengths).  One
 // work-group of 1024 threads, num_seqs <= 1024.
 __global__ void __launch_bounds__(1024) decode_order_kernel(const int* context_lens, int num_seqs, int width,
-                                                            int* order) {
+                                                            int pair_ok, int* sched) {
   constexpr int NC = 16;
   __shared__ int cnt[16][NC];   // [wave][class] members
+  __shared__ int wmin[16], wmax[16];
   const int b = threadIdx.x;
   const int wave = b >> 6, lane = b & 63;
   int cls = -1;
+  int len = 0;
   if (b < num_seqs) {
     const int ctx = context_lens[b];
-    const int len = ctx <= 0 ? width : (ctx < width ? ctx : width);
+    len = ctx <= 0 ? width : (ctx < width ? ctx : width);
     cls = (int)((long long)len * NC / ((long long)width + 1));
   }
   int before = 0;   // members of my class in my wave below my lane
@@ -93,14 +104,33 @@ __global__ void __launch_bounds__(1024) decode_order_kernel(const int* context_l
     if (lane == 0) cnt[wave][k] = __builtin_popcountll(m);
     if (cls == k) before = __builtin_popcountll(m & ((1ull << lane) - 1));
   }
+  int lo = b < num_seqs ? len : 0x7FFFFFFF, hi = b < num_seqs ? len : 0;
+#pragma unroll
+  for (int msk = 1; msk < 64; msk <<= 1) {
+    const int src = (lane ^ msk) << 2;
+    lo = min(lo, __builtin_amdgcn_ds_bpermute(src, lo));
+    hi = max(hi, __builtin_amdgcn_ds_bpermute(src, hi));
+  }
+  if (lane == 0) {
+    wmin[wave] = lo;
+    wmax[wave] = hi;
+  }
   __syncthreads();
+  if (b == 0) {
+    int mn = 0x7FFFFFFF, mx = 0;
+    for (int w = 0; w < 16; ++w) {
+      mn = min(mn, wmin[w]);
+      mx = max(mx, wmax[w]);
+    }
+    sched[0] = pair_ok && (long long)mx >= (long long)kDecodePairSpread * mn ? 2 : 1;
+  }
   if (b >= num_seqs) return;
   int rank = before;
   for (int w = 0; w < 16; ++w) {
 #pragma unroll
     for (int k = 0; k < NC; ++k) rank += (k > cls || (k == cls && w < wave)) ? cnt[w][k] : 0;
   }
-  order[rank] = b;
+  sched[1 + rank] = b;
 }
 
 }  // namespace tv

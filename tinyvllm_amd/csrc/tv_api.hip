@@ -88,7 +88,8 @@ int tv_abi_version(void) { return 3; }
 const char* tv_last_error(void) { return tv::last_error(); }
 
 // Unsplit launches of kDecodeOrderMinSeqs .. kDecodeOrderMaxSeqs sequences run
-// longest first (decode_order_kernel), which needs num_seqs ints of workspace.
+// longest first (decode_order_kernel, paged_decode_scheduled_kernel), which
+// needs num_seqs + 1 ints of workspace: KV heads per row, then the order.
 static constexpr int kDecodeOrderMinSeqs = 32;
 static constexpr int kDecodeOrderMaxSeqs = 1024;
 
@@ -101,7 +102,7 @@ size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim
   const long long parts = (width + partition_size - 1) / partition_size;
   if (parts <= 1)
     return num_seqs >= kDecodeOrderMinSeqs && num_seqs <= kDecodeOrderMaxSeqs
-               ? ((size_t)num_seqs * sizeof(int) + 255) & ~(size_t)255
+               ? ((size_t)(num_seqs + 1) * sizeof(int) + 255) & ~(size_t)255
                : 0;
   return (size_t)num_seqs * num_heads * parts * (head_dim + 2) * sizeof(float);
 }
@@ -175,16 +176,24 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
     return fail(TV_EINVAL, "tv_paged_decode: grid too large");
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  p.num_seqs = num_seqs;
+  bool pair = false;
   if (ordered) {
-    p.order = reinterpret_cast<int*>(workspace);
+    if (dtype == TV_F32) pair = tv::decode_pair_allowed<float>(p, head_dim, gt);
+    else if (dtype == TV_F16) pair = tv::decode_pair_allowed<_Float16>(p, head_dim, gt);
+    else pair = tv::decode_pair_allowed<__bf16>(p, head_dim, gt);
+  }
+  if (ordered) {
+    int* sched = reinterpret_cast<int*>(workspace);
+    p.sched = sched;
     hipLaunchKernelGGL(tv::decode_order_kernel, dim3(1), dim3(1024), 0, s, context_lens, num_seqs, (int)width,
-                       reinterpret_cast<int*>(workspace));
+                       pair ? 1 : 0, sched);
   }
   const dim3 grid(max_parts, num_kv_heads * p.head_chunks, num_seqs);
   bool launched = false;
-  if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, grid, s);
-  else if (dtype == TV_F16) launched = tv::launch_paged_decode<_Float16>(p, head_dim, gt, grid, s);
-  else launched = tv::launch_paged_decode<__bf16>(p, head_dim, gt, grid, s);
+  if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, pair, grid, s);
+  else if (dtype == TV_F16) launched = tv::launch_paged_decode<_Float16>(p, head_dim, gt, pair, grid, s);
+  else launched = tv::launch_paged_decode<__bf16>(p, head_dim, gt, pair, grid, s);
   if (!launched) return fail(TV_EUNSUPPORTED, "tv_paged_decode: no kernel for head_dim=%d gt=%d", head_dim, gt);
   int rc = check_launch("tv_paged_decode");
   if (rc != TV_OK || max_parts <= 1) return rc;
