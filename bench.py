@@ -38,10 +38,10 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
 # HBM bytes per launch of the primary decode (longest-first order kernel +
-# decode kernel) measured with two rocprofv3 --pmc passes (FETCH_SIZE x1.99994 +
+# decode kernel) measured with two rocprofv3 --pmc passes (FETCH_SIZE x1.99993 +
 # WRITE_SIZE x1.000, factors from a plain 1 GiB copy), recorded in
 # profiles/paged_decode_llama3_8b_f16.md.
-PRIMARY_TRAFFIC_BYTES = 2501426441
+PRIMARY_TRAFFIC_BYTES = 2500746870
 PRIMARY_TRAFFIC_SOURCE = "profiles/paged_decode_llama3_8b_f16.md"
 
 
