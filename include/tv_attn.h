@@ -58,6 +58,18 @@ size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim
                                        int max_blocks, int block_size, int partition_size);
 
 /*
+ * Partition size (tokens) for tv_paged_decode on the current device: the whole
+ * context (max_blocks*block_size rounded up to 16) when the batch gives at
+ * least 4 (sequence, KV head) work-groups per CU; otherwise the context split
+ * into as many partitions as make a full-width batch's work-groups fill the
+ * GPU's resident work-groups once (occupancy x CUs), rounded up to 16 tokens
+ * and at least 64.  No counterpart in the reference (which never splits);
+ * queries the device.  Returns 0 on bad arguments (see tv_last_error).
+ */
+int tv_paged_decode_partition_size(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                   int max_blocks, int block_size, int dtype);
+
+/*
  * Paged decode attention.  Replaces paged_decode_attention(...)
  * (tinyvllm/model/llama.py:97-144).
  *   out[b,0,h,:] = softmax_j((q[b,0,h,:] . K[j]) * scale) V[j]

@@ -24,6 +24,7 @@ SIGNATURES = {
     "tv_abi_version": (_I, []),
     "tv_last_error": (ctypes.c_char_p, []),
     "tv_paged_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),
+    "tv_paged_decode_partition_size": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "tv_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P, _S, _P]),
     "tv_flash_prefill_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "tv_flash_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _L, _I, _F, _I, _I,
@@ -47,7 +48,7 @@ SIGNATURES = {
     "tv_llama_prefill_workspace_bytes": (_S, [_P, _I]),
     "tv_llama_prefill": (_I, [_P, _P, _P, _P]),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 

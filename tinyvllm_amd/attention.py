@@ -15,9 +15,6 @@ from . import _lib
 
 _lib.load()
 
-DEFAULT_PARTITION = 2048
-
-
 def _require(cond, msg):
     if not cond:
         raise ValueError(msg)
@@ -31,22 +28,20 @@ def _on_gpu(*tensors):
     return dev
 
 
-def default_partition_size(num_seqs, num_kv_heads, width, num_cus=256):
-    """Tokens per decode work-group (multiple of 16).
+def default_partition_size(num_seqs, n_heads, n_kv_heads, head_dim, max_blocks, block_size, dtype):
+    """Tokens per decode work-group (multiple of 16) for this shape on the current device.
 
     With at least four (sequence, KV head) pairs per CU the work-groups already
     fill the GPU, and splitting only adds partial writes and a merge launch, so
     each pair gets one work-group over its whole context.  Otherwise contexts
-    are split into partitions of up to 2048 tokens (long partitions amortise a
-    work-group's fixed cost; 2048 measured fastest on MI355X for 16 x 32768),
-    halved while there would be fewer than two work-groups per CU.
+    are split into as many partitions as make a full-width batch's work-groups
+    fill the resident work-group slots once (occupancy x CUs, queried by the
+    library): on MI355X 16 x 32768 bf16 runs 323 us with 5472-token partitions
+    (768 work-groups, one round) against 342 us with 2048.
     """
-    pairs = max(1, num_seqs * num_kv_heads)
-    if pairs >= 4 * num_cus:
-        return max(16, (width + 15) // 16 * 16)
-    p = DEFAULT_PARTITION
-    while p > 64 and pairs * ((width + p - 1) // p) < 2 * num_cus:
-        p //= 2
+    p = _lib.load().tv_paged_decode_partition_size(num_seqs, n_heads, n_kv_heads, head_dim, max_blocks,
+                                                     block_size, _lib.dtype_code(dtype))
+    _lib.check(0 if p > 0 else _lib.TV_EINVAL, "default_partition_size")
     return p
 
 
@@ -87,7 +82,7 @@ def paged_decode_attention(queries, k_cache, v_cache, block_tables, context_lens
     _require(used > 0, "no block table columns to attend over")
     width = used * block_size
     if partition_size is None:
-        partition_size = default_partition_size(b, n_kv_heads, width)
+        partition_size = default_partition_size(b, n_heads, n_kv_heads, head_dim, used, block_size, queries.dtype)
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     out = torch.empty((b, 1, hq, d), dtype=out_dtype, device=dev)
     ws_bytes = lib.tv_paged_decode_workspace_bytes(b, hq, d, used, block_size, partition_size)
@@ -163,7 +158,8 @@ class PagedDecodePlan:
         used = mb if max_context_len is None else min((int(max_context_len) + block_size - 1) // block_size, mb)
         _require(used > 0, "no block table columns to attend over")
         if partition_size is None:
-            partition_size = default_partition_size(b, n_kv_heads, used * block_size)
+            partition_size = default_partition_size(b, n_heads, n_kv_heads, head_dim, used, block_size,
+                                                    queries.dtype)
         self.partition_size = int(partition_size)
         out_dtype = queries.dtype if out_dtype is None else out_dtype
         # validate once through the functional path's checks

@@ -32,6 +32,28 @@ int scheduled_pair_slots() {
   return cache[dev];
 }
 
+// Work-groups of the partitioned kernel (uniform-tile form) resident at once on
+// the current device (occupancy x CUs), queried once per device and instantiation.
+template <typename T, int D, int GT>
+int partitioned_slots() {
+  static int cache[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cache[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<T, D, GT, kDecodeWaves, true>,
+                                                     64 * kDecodeWaves, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    cache[dev] = per_cu * cus;
+  }
+  return cache[dev];
+}
+
+template <typename T>
+int decode_partitioned_slots(int head_dim, int gt);
+
 // Whether a scheduled launch may pair KV heads: Hkv even and at least 5/4
 // paired items per resident work-group, so that the longest-first order still
 // has short items left to fill the end of the launch (with fewer, pairing
@@ -96,7 +118,24 @@ bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, bool pair,
   TV_DECODE_PAIR_CASE(T, D, 4)      \
   TV_DECODE_PAIR_CASE(T, D, 8)
 
+#define TV_DECODE_SLOTS_CASE(T, D, GT) \
+  if (head_dim == D && gt == GT) return partitioned_slots<T, D, GT>();
+#define TV_DECODE_SLOTS_ALL_GT(T, D) \
+  TV_DECODE_SLOTS_CASE(T, D, 1)      \
+  TV_DECODE_SLOTS_CASE(T, D, 2)      \
+  TV_DECODE_SLOTS_CASE(T, D, 4)      \
+  TV_DECODE_SLOTS_CASE(T, D, 8)
+
 #define TV_DECODE_DEFINE(T)                                                                      \
+  template <>                                                                                    \
+  int decode_partitioned_slots<T>(int head_dim, int gt) {                                        \
+    TV_DECODE_SLOTS_ALL_GT(T, 16)                                                                \
+    TV_DECODE_SLOTS_ALL_GT(T, 32)                                                                \
+    TV_DECODE_SLOTS_ALL_GT(T, 64)                                                                \
+    TV_DECODE_SLOTS_ALL_GT(T, 128)                                                               \
+    TV_DECODE_SLOTS_ALL_GT(T, 256)                                                               \
+    return 0;                                                                                    \
+  }                                                                                              \
   template <>                                                                                    \
   bool decode_pair_allowed<T>(const DecodeParams& p, int head_dim, int gt) {                     \
     TV_DECODE_PAIR_ALL_GT(T, 16)                                                                 \

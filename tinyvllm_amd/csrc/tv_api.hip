@@ -83,7 +83,7 @@ int vec_width(std::initializer_list<long long> sizes, std::initializer_list<cons
 
 extern "C" {
 
-int tv_abi_version(void) { return 3; }
+int tv_abi_version(void) { return 4; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
@@ -105,6 +105,33 @@ size_t tv_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim
                ? ((size_t)(num_seqs + 1) * sizeof(int) + 255) & ~(size_t)255
                : 0;
   return (size_t)num_seqs * num_heads * parts * (head_dim + 2) * sizeof(float);
+}
+
+int tv_paged_decode_partition_size(int num_seqs, int num_heads, int num_kv_heads, int head_dim, int max_blocks,
+                                   int block_size, int dtype) {
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || max_blocks <= 0 ||
+      block_size <= 0 || !valid_dtype(dtype))
+    return fail(TV_EINVAL, "tv_paged_decode_partition_size: bad arguments"), 0;
+  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(TV_EUNSUPPORTED, "tv_paged_decode_partition_size: head_dim %d not supported", head_dim), 0;
+  const long long width = (long long)max_blocks * block_size;
+  const int whole = (int)((width + 15) / 16 * 16);
+  const int group = num_heads / num_kv_heads;
+  const int gt = heads_per_group_chunk(group);
+  const long long rows = (long long)num_seqs * num_kv_heads * (group / gt);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess || cus < 1)
+    return fail(TV_EHIP, "tv_paged_decode_partition_size: no device"), 0;
+  if (rows >= 4LL * cus) return whole;
+  const int slots = dtype == TV_F32   ? tv::decode_partitioned_slots<float>(head_dim, gt)
+                    : dtype == TV_F16 ? tv::decode_partitioned_slots<_Float16>(head_dim, gt)
+                                      : tv::decode_partitioned_slots<__bf16>(head_dim, gt);
+  const long long parts = ((long long)slots + rows - 1) / rows;
+  long long p = (width + parts - 1) / parts;
+  p = (p + 15) / 16 * 16;
+  if (p < 64) p = 64;
+  return p < whole ? (int)p : whole;
 }
 
 int tv_paged_decode(void* out, const void* queries, const void* k_cache, const void* v_cache,

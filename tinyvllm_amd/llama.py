@@ -373,8 +373,8 @@ class DecodeGraph:
         self.logits = torch.zeros((batch, c.vocab_size), dtype=torch.float32, device=dev) if keep_logits else None
         self.history_len = history_len
         self.history = torch.zeros((batch, history_len), dtype=torch.int32, device=dev) if history_len else None
-        self.partition_size = partition_size or default_partition_size(batch, c.n_kv_heads,
-                                                                       max_blocks * kv_cache.block_size)
+        self.partition_size = partition_size or default_partition_size(batch, c.n_heads, c.n_kv_heads, c.head_dim,
+                                                                       max_blocks, kv_cache.block_size, c.dtype)
         lib = _lib.load()
         need = lib.tv_llama_decode_workspace_bytes(ctypes.byref(model._model), batch, max_blocks,
                                                    kv_cache.block_size, self.partition_size)
