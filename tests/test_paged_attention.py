@@ -198,6 +198,23 @@ def test_scheduled_launch_group_shapes(hq, hkv, d):
     check(case, hq, hkv, d, 16, torch.float16)
 
 
+def test_partition_size_recommendation():
+    """tv_paged_decode_partition_size: whole context when the batch fills the
+    GPU, else partitions that make a full-width batch's work-groups fill the
+    resident work-group slots once; a multiple of 16, at least 64."""
+    from tinyvllm_amd.attention import default_partition_size
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    whole = default_partition_size(4 * cus // 8, 32, 8, 128, 256, 16, torch.float16)
+    assert whole == 4096
+    p = default_partition_size(16, 32, 8, 128, 2048, 16, torch.bfloat16)
+    assert p % 16 == 0 and 64 <= p < 32768
+    parts = -(-32768 // p)
+    assert 16 * 8 * parts >= cus                    # at least one work-group per CU
+    assert default_partition_size(4, 32, 4, 64, 16, 16, torch.float32) == 64
+    with pytest.raises(ValueError):
+        default_partition_size(4, 30, 4, 64, 16, 16, torch.float32)
+
+
 def test_deterministic():
     case = build_case(11, [100, 700, 3], 32, 8, 128, 16, torch.float16)
     a = run(*case, 32, 8, 128, 16, partition_size=128)
