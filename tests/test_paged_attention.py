@@ -215,6 +215,37 @@ def test_partition_size_recommendation():
         default_partition_size(4, 30, 4, 64, 16, 16, torch.float32)
 
 
+def test_scheduled_launch_in_graph():
+    """The scheduled launch (schedule kernel + paired decode) captured in a HIP
+    graph on its first use: every replay, with eager work and synchronisation
+    between replays, matches the eager result and the oracle."""
+    from tinyvllm_amd.attention import PagedDecodePlan
+    rng = np.random.Generator(np.random.PCG64(31))
+    ctx = rng.integers(1, 150, 256).astype(np.int32)
+    q, kc, vc, bt, cl = build_case(32, ctx.tolist(), 32, 8, 64, 16, torch.float16, width=10)
+    dev = "cuda"
+    args = [q.to(dev), kc.to(dev), vc.to(dev), torch.from_numpy(bt).to(dev), torch.from_numpy(cl).to(dev)]
+    plan = PagedDecodePlan(*args, 32, 8, 64, 16)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            plan.run()
+    torch.cuda.synchronize()
+    want = oracle(q, kc, vc, bt, cl, 32, 8, 64, 16)
+    eager = PagedDecodePlan(*args, 32, 8, 64, 16).run().clone()
+    torch.cuda.synchronize()
+    assert np.abs(eager.float().cpu().numpy() - want).max() <= 2e-2
+    for _ in range(3):
+        plan.out.zero_()
+        junk = torch.randn(1 << 20, device=dev).sum()    # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.out, eager)
+        del junk
+
+
 def test_deterministic():
     case = build_case(11, [100, 700, 3], 32, 8, 128, 16, torch.float16)
     a = run(*case, 32, 8, 128, 16, partition_size=128)
