@@ -187,7 +187,15 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* ptr) {
 // Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit dwords, no
 // swizzle).  A load whose voffset lies at or past `bytes` returns zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned long long bytes) {
-  const unsigned n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (unsigned)bytes;
+  // Clamp to 32 bits with a scalar compare of the high word.  Written as C the
+  // compiler folds it into a 64-bit unsigned compare, which has no scalar form
+  // and costs three VALU instructions per resource (bytes is wave-uniform at
+  // every call, so both halves are scalars).
+  unsigned n;
+  asm("s_cmp_lg_u32 %1, 0\n\ts_cselect_b32 %0, -1, %2"
+      : "=s"(n)
+      : "s"((unsigned)(bytes >> 32)), "s"((unsigned)bytes)
+      : "scc");
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
