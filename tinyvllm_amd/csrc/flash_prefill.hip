@@ -260,7 +260,7 @@ prefill_fa_kernel(const PrefillParams p) {
     mref[r] = 0.0f;
     thr[r] = -__FLT_MAX__;
   }
-  const u32x4 ones = u32x4{kOnes2<T>, kOnes2<T>, kOnes2<T>, kOnes2<T>};
+  u32x4 ones = u32x4{kOnes2<T>, kOnes2<T>, kOnes2<T>, kOnes2<T>};
 
   auto compute = [&](int b, int t) {
     const uint16_t* sk = tiles + b * BUF;
@@ -303,15 +303,21 @@ prefill_fa_kernel(const PrefillParams p) {
             st[r][kb][i] = k0 + kb * 16 + 4 * g + i <= lim ? st[r][kb][i] : kNegInf;
       }
     }
-    float mt[RB];
+    // Each lane tests its own keys against the threshold; a query's maximum
+    // over the tile exceeds it exactly when one of its four lanes' does, so
+    // the cross-lane maximum is only formed on the (rare) rescale path.
+    float lm[RB];
     bool need_any = false;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      mt[r] = max_over_g(max_tile<KB>(st[r]));
-      need_any = need_any || mt[r] > thr[r];
+      lm[r] = max_tile<KB>(st[r]);
+      need_any = need_any || lm[r] > thr[r];
     }
     if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
       __asm__ volatile("" ::: "memory");
+      float mt[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) mt[r] = max_over_g(lm[r]);
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const bool need = mt[r] > thr[r];
@@ -343,6 +349,9 @@ prefill_fa_kernel(const PrefillParams p) {
         for (int db = 0; db < DB; ++db) oacc[r][db] = mfma16x16x32<T>(vf[db][ks2], pf[r][ks2], oacc[r][db]);
         oacc[r][DB] = mfma16x16x32<T>(ones, pf[r][ks2], oacc[r][DB]);
       }
+    // opaque to the optimiser: keeps the ones vector in its registers across
+    // steps instead of rebuilding it (three moves) after they are reused
+    __asm__ volatile("" : "+v"(ones));
   };
 
   // group tile sequence grp + KS j; steps padded to even so the loop body
