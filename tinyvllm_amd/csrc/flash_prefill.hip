@@ -295,12 +295,14 @@ prefill_fa_kernel(const PrefillParams p) {
     if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0))) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        const int lim = p.causal ? min(klim - 1, qi[r]) : klim - 1;   // last visible key
+        // last visible key, relative to this lane's first key k0 + 4 g: each
+        // element is then one compare against a constant and one select
+        const int rel = (p.causal ? min(klim - 1, qi[r]) : klim - 1) - (k0 + 4 * g);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            st[r][kb][i] = k0 + kb * 16 + 4 * g + i <= lim ? st[r][kb][i] : kNegInf;
+            st[r][kb][i] = kb * 16 + i <= rel ? st[r][kb][i] : kNegInf;
       }
     }
     // Each lane tests its own keys against the threshold; a query's maximum
