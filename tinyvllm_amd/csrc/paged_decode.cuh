@@ -2,16 +2,18 @@
 // block-paged K/V cache [num_blocks, block_size, Hkv, D].
 //
 // Work decomposition
-//   grid.x = context partition, grid.y = (KV head, query-head chunk), grid.z =
-//   sequence.  A work-group of NW waves handles one KV head -- or, in a
-//   scheduled launch with head pairs, two adjacent KV heads -- each for GT
-//   query heads of its GQA group, so
-//   every K/V row fetched from HBM is used by GT query heads.  With hpw heads
-//   per work-group wave w serves head w % hpw; the NW / hpw waves of a head
-//   take interleaved tiles of TT tokens inside the partition, and the waves of
-//   the hpw heads read the same tokens together (hpw * D contiguous elements of
-//   each cache row [token, Hkv, D]).
-//
+//   A work-group of NW waves attends one sequence for one KV head -- or two
+//   adjacent KV heads (hpw = 2) -- each for GT query heads of its GQA group, so
+//   every K/V row fetched from HBM is used by GT query heads.  Wave w serves
+//   head w % hpw; the NW / hpw waves of a head take interleaved tiles of TT
+//   tokens, and with two heads the waves read the same tokens together (2 D
+//   contiguous elements of each cache row [token, Hkv, D]).
+//   paged_decode_kernel: grid (context partition, KV head x query-head chunk,
+//   sequence), one KV head per work-group; partitions of a split context
+//   leave partials for paged_decode_reduce_kernel.
+//   paged_decode_scheduled_kernel: 1-D grid over (sequence, row) items in the
+//   longest-first order of decode_order_kernel, which also picks hpw.
+
 // Lane layout inside a wave
 //   A cache row (one token, one KV head) is D*sizeof(T) bytes.  LPR lanes cover
 //   one row with 16-byte loads (VPL vectors each), so one load instruction
@@ -23,7 +25,8 @@
 //   Split-context partials (m, l, o) go to the caller's workspace and a second
 //   kernel merges them (flash-decoding).
 //   When a cache block holds whole tiles (block_size % 16 == 0) each tile needs
-//   a single wave-uniform block-table lookup.
+//   a single wave-uniform block-table lookup, and its rows are read through a
+//   buffer resource whose range ends at the tile's last attended row.
 //
 // Semantics follow tinyvllm/model/llama.py:97-144: scores are (q.k)*scale,
 // positions >= context_len are excluded (the reference adds -1e9, which
