@@ -188,14 +188,16 @@ def test_scheduled_launch_many_sequences(spread, dtype):
     check((q, kc, vc, bt, cl), 32, 8, 128, 16, dtype)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(32, 4, 64), (16, 2, 128), (24, 6, 64)])
-def test_scheduled_launch_group_shapes(hq, hkv, d):
-    """Scheduled launches over several GQA shapes (Hkv / 2 pairs per sequence
-    when the item count and the length spread allow it)."""
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 4, 64, torch.float16), (16, 2, 128, torch.float16),
+                                            (24, 6, 64, torch.float16), (32, 4, 64, torch.float32),
+                                            (32, 8, 128, torch.bfloat16)])
+def test_scheduled_launch_group_shapes(hq, hkv, d, dtype):
+    """Scheduled launches over several GQA shapes and dtypes (Hkv / 2 pairs per
+    sequence when the item count and the length spread allow it)."""
     rng = np.random.Generator(np.random.PCG64(23))
     ctx = rng.integers(1, 120, 900).astype(np.int32)
-    case = build_case(24, ctx.tolist(), hq, hkv, d, 16, torch.float16, width=8)
-    check(case, hq, hkv, d, 16, torch.float16)
+    case = build_case(24, ctx.tolist(), hq, hkv, d, 16, dtype, width=8)
+    check(case, hq, hkv, d, 16, dtype)
 
 
 def test_partition_size_recommendation():
