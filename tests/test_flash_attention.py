@@ -186,3 +186,35 @@ def test_mfma_split_rows_merge(chunk_tiles, lq, causal, dtype):
                 chunk_tiles=chunk_tiles)[0]
     want = flash_prefill_ref(q.float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None], causal)[0]
     assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-2
+
+
+# ---- seeded random shapes -------------------------------------------------------------
+
+def _random_prefill_cases(n=24, seed=71):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cases = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        hq = hkv * int(rng.choice([1, 2, 4, 8]))
+        d = int(rng.choice([64, 128, 64, 128, 32, 80]))
+        lq = int(rng.integers(1, 700))
+        lk = lq if rng.random() < 0.7 else int(rng.integers(1, 700))
+        causal = bool(rng.random() < 0.7)
+        dtype = [torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))]
+        chunk = int(rng.choice([0, 0, 0, 1, 2, 4]))
+        cases.append((i, hq, hkv, d, lq, lk, causal, dtype, chunk))
+    return cases
+
+
+@pytest.mark.parametrize("i,hq,hkv,d,lq,lk,causal,dtype,chunk", _random_prefill_cases())
+def test_random_shapes(i, hq, hkv, d, lq, lk, causal, dtype, chunk):
+    """Seeded random head counts, head dims (MFMA and generic), lengths
+    (Lq != Lk included), masks, dtypes and key-chunk splits against the oracle."""
+    q = randn(300 + i, lq, hq, d, dtype=dtype)
+    k = randn(400 + i, lk, hkv, d, dtype=dtype)
+    v = randn(500 + i, lk, hkv, d, dtype=dtype)
+    out = _op()(q.unsqueeze(0).cuda(), k.unsqueeze(0).cuda(), v.unsqueeze(0).cuda(), causal,
+                chunk_tiles=chunk)[0]
+    torch.cuda.synchronize()
+    want = flash_prefill_ref(q.float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None], causal)[0]
+    assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]

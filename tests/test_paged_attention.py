@@ -272,3 +272,35 @@ def test_rejects_bad_arguments():
     with pytest.raises(ValueError):
         _ops()(q.to(dev), kc.to(dev), vc.to(dev), torch.from_numpy(bt).to(dev),
                torch.from_numpy(cl).to(dev), 8, 4, 64, 16)
+
+
+# ---- seeded random shapes -------------------------------------------------------------
+
+def _random_decode_cases(n=24, seed=81):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cases = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        hq = hkv * int(rng.choice([1, 2, 3, 4, 8]))
+        d = int(rng.choice([16, 32, 64, 128, 256]))
+        bs = int(rng.choice([16, 16, 32, 8, 1, 12]))
+        b = int(rng.choice([1, 3, 17, 40, 64, 300]))
+        width = int(rng.integers(1, 40))            # table columns
+        while b > 1 and b * width * bs * hkv * d > (8 << 20):   # keeps the float64 oracle small
+            b //= 2
+        ctx = rng.integers(0, width * bs + 40, b)   # zero, short, past the table
+        dtype = [torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))]
+        psize = [None, None, 16, 64, 512][int(rng.integers(0, 5))]
+        cases.append((i, hq, hkv, d, bs, width, ctx.astype(np.int32), dtype, psize))
+    return cases
+
+
+@pytest.mark.parametrize("i,hq,hkv,d,bs,width,ctx,dtype,psize", _random_decode_cases())
+def test_random_shapes(i, hq, hkv, d, bs, width, ctx, dtype, psize):
+    """Seeded random batches, GQA shapes, head dims, block sizes, table widths,
+    context lengths (0 and past the table included), dtypes and partition
+    sizes against the oracle."""
+    q, kc, vc, bt, _ = build_case(600 + i, [max(1, min(int(c), width * bs)) for c in ctx], hq, hkv, d, bs,
+                                  dtype, width=width)
+    kw = {} if psize is None else {"partition_size": psize}
+    check((q, kc, vc, bt, ctx), hq, hkv, d, bs, dtype, **kw)
