@@ -133,8 +133,8 @@ def bench_prefill(steps, warmup):
     import torch
     from tinyvllm_amd.attention import PrefillPlan
     from tinyvllm_amd.kv_cache import reshape_and_cache
-    from tinyvllm_amd.workloads import config2_prefill_tinyllama
-    wl = config2_prefill_tinyllama()
+    from tinyvllm_amd.workloads import prefill_tinyllama_l512_l1024
+    wl = prefill_tinyllama_l512_l1024()
     plans = [PrefillPlan(q, k, v, True) for q, k, v in zip(wl.q, wl.k, wl.v)]
     per = [timed(p.run, steps, warmup, graph=True) for p in plans]
     kc = torch.zeros((wl.num_blocks, 16, 4, 64), dtype=torch.float16, device="cuda")
@@ -177,7 +177,7 @@ def bench_e2e(decode_steps=128, warmup=3):
     import torch
     from tinyvllm_amd import workloads
     from tinyvllm_amd.llama import DecodeGraph
-    wl = workloads.config4_e2e_tinyllama(decode_steps=decode_steps)
+    wl = workloads.e2e_tinyllama_b64(decode_steps=decode_steps)
     m, kv = wl.model, wl.kv
     B, L = wl.batch, wl.prompt_len
     first = torch.zeros(B, dtype=torch.int32, device="cuda")
@@ -239,7 +239,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
-                 "(the attention hot path shards by sequence or KV head with no exchange; see DESIGN.md)")
+                 "(the attention hot path shards by sequence or KV head with no exchange)")
 
     import torch
     from tinyvllm_amd import workloads
@@ -251,34 +251,34 @@ def main():
     if args.prefill_only:
         print(json.dumps(bench_prefill(args.steps, args.warmup)), flush=True)
         return
-    log("bench: config3 decode (B256 Hq32 Hkv8 D128 fp16)")
-    wl3 = workloads.config3_decode_llama3_8b()
+    log("bench: paged decode B256 Hq32 Hkv8 D128 fp16")
+    wl3 = workloads.decode_llama3_8b_b256()
     torch.cuda.synchronize()
     r3 = bench_decode(wl3, args.steps, args.warmup, graph=False)
-    log(f"bench: config3 {r3['ms']:.4f} ms {r3['gbs']:.1f} GB/s")
+    log(f"bench: paged decode B256 {r3['ms']:.4f} ms {r3['gbs']:.1f} GB/s")
 
     configs = {}
     if not args.primary_only:
-        log("bench: config1 decode (TinyLlama fp32)")
-        wl1 = workloads.config1_decode_tinyllama()
+        log("bench: paged decode TinyLlama fp32 B4")
+        wl1 = workloads.decode_tinyllama_f32_b4()
         r1 = bench_decode(wl1, args.steps, args.warmup, graph=True)
         configs["decode_tinyllama_f32_b4"] = {
             "value": round(r1["ms"] * 1e3, 3), "unit": "us", "gbs": round(r1["gbs"], 1),
             "bytes": r1["bytes"], "note": "cache-resident (~1 MB): latency-bound, not an HBM figure"}
         del wl1
-        log("bench: config2 prefill")
+        log("bench: causal prefill TinyLlama shape L512 + L1024 (and Llama-3-8B heads L2048)")
         configs["prefill_tinyllama_f16"] = bench_prefill(args.steps, args.warmup)
-        log("bench: config5 long split decode (B16 x 32768 bf16)")
-        wl5 = workloads.config5_decode_long()
+        log("bench: split-context decode B16 x 32768 bf16")
+        wl5 = workloads.decode_long_bf16_b16()
         r5 = bench_decode(wl5, max(10, args.steps // 2), args.warmup, graph=False)
         configs["decode_long_bf16_b16_32k"] = {
             "value": round(r5["gbs"], 1), "unit": "GB/s", "ms": round(r5["ms"], 4),
             "frac_of_hbm_peak": round(r5["gbs"] / HBM_PEAK_GBS, 4), "bytes": r5["bytes"],
             "partition_size": r5["partition_size"]}
         del wl5
-        log("bench: config4 end-to-end TinyLlama decode (B64, ctx 1024, 128 steps)")
+        log("bench: TinyLlama-1.1B greedy decode B64, prompts 1024, 128 steps")
         configs["e2e_tinyllama_decode"] = bench_e2e()
-        log(f"bench: config4 {configs['e2e_tinyllama_decode']['value']} tok/s")
+        log(f"bench: TinyLlama decode {configs['e2e_tinyllama_decode']['value']} tok/s")
 
     if args.calib_copy_mib:
         n = args.calib_copy_mib << 20

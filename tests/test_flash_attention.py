@@ -111,8 +111,8 @@ def test_mfma_path(dtype, d, lq, causal):
 
 
 @pytest.mark.parametrize("length", [512, 1024])
-def test_tinyllama_prefill_config2(length):
-    """Config 2 shape: Hq 32, Hkv 4, D 64, fp16 inputs, causal."""
+def test_tinyllama_prefill_shape(length):
+    """TinyLlama prefill shape: Hq 32, Hkv 4, D 64, fp16 inputs, causal."""
     q, k, v = (randn(30 + i, length, 32 if i == 0 else 4, 64, dtype=torch.float16) for i in range(3))
     check(q, k, v)
 

@@ -113,10 +113,10 @@ def test_split_context_partitions(psize, dtype):
     check(case, 16, 4, 128, 16, dtype, partition_size=psize)
 
 
-def test_tinyllama_config1_workload():
-    """Config 1: TinyLlama layer, fp32, ctx {17,64,128,250}, shuffled 64-block pool."""
-    from tinyvllm_amd.workloads import config1_decode_tinyllama
-    wl = config1_decode_tinyllama(device="cuda")
+def test_tinyllama_b4_fp32_workload():
+    """TinyLlama layer, fp32, B4, ctx {17,64,128,250}, shuffled 64-block pool."""
+    from tinyvllm_amd.workloads import decode_tinyllama_f32_b4
+    wl = decode_tinyllama_f32_b4(device="cuda")
     out = _ops()(wl.q, wl.k_cache, wl.v_cache, wl.bt_dev, wl.ctx_dev, 32, 4, 64, 16)
     want = paged_decode_ref(wl.host["q"], wl.host["k_cache"], wl.host["v_cache"], wl.block_tables,
                             wl.context_lens, 32, 4, 64, 16)

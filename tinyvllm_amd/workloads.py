@@ -107,13 +107,13 @@ def make_decode(name, context_lens, num_heads, num_kv_heads, head_dim, block_siz
 
 # ---- the benchmark configurations ---------------------------------------------
 
-def config1_decode_tinyllama(device="cuda", seed=0):
+def decode_tinyllama_f32_b4(device="cuda", seed=0):
     """Paged decode, TinyLlama layer shape, fp32, B=4, ctx {17,64,128,250}, 64-block pool."""
     return make_decode("decode_tinyllama_f32_b4", [17, 64, 128, 250], 32, 4, 64, 16, torch.float32,
                        pool=64, seed=seed, device=device)
 
 
-def config3_decode_llama3_8b(device="cuda", seed=0, batch=256, host_ok=False):
+def decode_llama3_8b_b256(device="cuda", seed=0, batch=256, host_ok=False):
     """Paged decode, Llama-3-8B head shape, fp16, B=256, ctx ~ U[512, 4096], pool +10%."""
     rng = np.random.Generator(np.random.PCG64(seed))
     ctx = rng.integers(512, 4097, batch).astype(np.int32)
@@ -121,7 +121,7 @@ def config3_decode_llama3_8b(device="cuda", seed=0, batch=256, host_ok=False):
                        max_blocks=4096 // 16, seed=seed, device=device, host_ok=host_ok, rng=rng)
 
 
-def config5_decode_long(device="cuda", seed=0, batch=16, context=32768, host_ok=False):
+def decode_long_bf16_b16(device="cuda", seed=0, batch=16, context=32768, host_ok=False):
     """Split-context paged decode, Llama-3-8B head shape, bf16, B=16 x ctx 32768."""
     return make_decode("decode_long_bf16_b16_32k", [context] * batch, 32, 8, 128, 16, torch.bfloat16,
                        max_blocks=context // 16, seed=seed, device=device, host_ok=host_ok)
@@ -163,7 +163,7 @@ class PrefillWorkload:
         return 2 * t * self.num_kv_heads * self.head_dim * es * 2 + t * 4
 
 
-def config2_prefill_tinyllama(device="cuda", seed=0, lengths=(512, 1024), spare_blocks=8):
+def prefill_tinyllama_l512_l1024(device="cuda", seed=0, lengths=(512, 1024), spare_blocks=8):
     """Causal prefill + KV write, TinyLlama shape, fp16, prompts of 512 and 1024 tokens."""
     rng = np.random.Generator(np.random.PCG64(seed))
     bs = 16
@@ -217,7 +217,7 @@ class E2EWorkload:
         return sum(self.weight_bytes_per_step() + self.kv_bytes(first_ctx + i) for i in range(steps))
 
 
-def config4_e2e_tinyllama(device="cuda", seed=0, batch=64, prompt_len=1024, decode_steps=128, block_size=16,
+def e2e_tinyllama_b64(device="cuda", seed=0, batch=64, prompt_len=1024, decode_steps=128, block_size=16,
                           pool_margin=0.1):
     """Random-init TinyLlama-1.1B (fp16 weights ~ N(0, 0.02), unit norms), ``batch``
     prompts of ``prompt_len`` seeded token ids, blocks for prompt + decode drawn from
