@@ -51,7 +51,11 @@ def f64(t):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K,ks", [(1, 64, 32, 32), (5, 100, 96, 32), (64, 2560, 2048, 256),
                                       (70, 132, 320, 64), (130, 64, 512, 512), (64, 2048, 5632, 768),
-                                      (3, 40, 800, 800)])
+                                      (3, 40, 800, 800),
+                                      # whole 256-wide chunks (direct-to-LDS A): ragged N and M, 1-5 chunks
+                                      # per split, padded pipeline steps, a short last split
+                                      (33, 100, 1024, 512), (64, 2048, 5632, 1024), (17, 84, 1280, 1280),
+                                      (64, 148, 2560, 768)])
 def test_linear_partial(dtype, M, N, K, ks):
     from tinyvllm_amd._lib import dtype_code
     a = gen(1, M, K, dtype=dtype)
@@ -66,20 +70,23 @@ def test_linear_partial(dtype, M, N, K, ks):
         assert np.abs(P[s] - want).max() < 1e-4 * max(1.0, np.abs(want).max()), s
 
 
-def test_linear_strided_a():
+@pytest.mark.parametrize("K,lda,ks", [(96, 160, 96), (512, 776, 256)])
+def test_linear_strided_a(K, lda, ks):
     """A rows at a stride larger than K (a view into a wider activation buffer)."""
     from tinyvllm_amd._lib import TV_F16
-    big = gen(3, 9, 160)
-    a = big[:, :96]
-    w = gen(4, 64, 96, scale=0.05)
-    part = torch.empty((1, 9, 64), dtype=torch.float32, device="cuda")
-    check(lib().tv_linear(ptr(part), ptr(a), ptr(w), 9, 64, 96, 160, 0, 96, 0, None, TV_F16, None), "linear")
+    big = gen(3, 9, lda)
+    a = big[:, :K]
+    w = gen(4, 64, K, scale=0.05)
+    splits = -(-K // ks)
+    part = torch.empty((splits, 9, 64), dtype=torch.float32, device="cuda")
+    check(lib().tv_linear(ptr(part), ptr(a), ptr(w), 9, 64, K, lda, 0, ks, 0, None, TV_F16, None), "linear")
     torch.cuda.synchronize()
-    assert np.abs(part[0].double().cpu().numpy() - f64(a) @ f64(w).T).max() < 1e-4
+    want = f64(a) @ f64(w).T
+    assert np.abs(part.sum(0).double().cpu().numpy() - want).max() < 1e-4 * max(1.0, np.abs(want).max())
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,H,K", [(4, 48, 64), (64, 5632, 2048), (65, 96, 256)])
+@pytest.mark.parametrize("M,H,K", [(4, 48, 64), (64, 5632, 2048), (65, 96, 256), (16, 40, 4096)])
 def test_linear_swiglu(dtype, M, H, K):
     from tinyvllm_amd._lib import dtype_code
     a = gen(5, M, K, dtype=dtype)
@@ -95,7 +102,7 @@ def test_linear_swiglu(dtype, M, H, K):
     assert np.abs(out.double().cpu().numpy() - want).max() < TOL * max(1.0, np.abs(want).max())
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 100, 64), (64, 32000, 2048), (70, 260, 96)])
+@pytest.mark.parametrize("M,N,K", [(3, 100, 64), (64, 32000, 2048), (70, 260, 96), (70, 260, 768)])
 def test_linear_logits_and_greedy(M, N, K):
     from tinyvllm_amd._lib import TV_F16
     a = gen(8, M, K)
