@@ -14,8 +14,10 @@
  *
  * Conventions are those of tv_attn.h (device pointers, caller-owned buffers,
  * stream = hipStream_t, return 0 or a TV_E* code with tv_last_error()).
- * dtype is TV_F16 or TV_BF16 for everything in this header: the products run
- * on MFMA.  Norm weights and the RoPE table are float32.
+ * dtype is TV_F16, TV_BF16 or TV_F32 (the reference's default model dtype,
+ * weights.py:32) for everything in this header: the products run on MFMA
+ * (v_mfma_f32_16x16x32 for 16-bit types, v_mfma_f32_16x16x4_f32 for fp32).
+ * Norm weights and the RoPE table are float32.
  */
 #ifndef TV_LLAMA_H
 #define TV_LLAMA_H

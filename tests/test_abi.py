@@ -132,7 +132,7 @@ def test_dense_entry_points_validate_on_host():
     # K not a multiple of 32, N not a multiple of 4, bad dtype, multi-split logits
     assert lib.tv_linear(p, p, p, 4, 64, 48, 48, 0, 48, 0, None, _lib.TV_F16, None) == _lib.TV_EUNSUPPORTED
     assert lib.tv_linear(p, p, p, 4, 66, 64, 64, 0, 64, 0, None, _lib.TV_F16, None) == _lib.TV_EUNSUPPORTED
-    assert lib.tv_linear(p, p, p, 4, 64, 64, 64, 0, 64, 0, None, _lib.TV_F32, None) == _lib.TV_EUNSUPPORTED
+    assert lib.tv_linear(p, p, p, 4, 64, 64, 64, 0, 64, 0, None, 7, None) == _lib.TV_EUNSUPPORTED   # no such dtype
     assert lib.tv_linear(p, p, p, 4, 64, 64, 64, 64, 32, 2, None, _lib.TV_F16, None) == _lib.TV_EINVAL
     assert b"one split" in lib.tv_last_error()
     assert lib.tv_qkv_rope_cache(p, None, None, p, None, p, 1, None, 0, p, 8, p, 0, 1, 16, 4, 1, 4, 2, 16,

@@ -3,8 +3,9 @@
 Kernel level (through the C ABI, include/tv_llama.h): the skinny MFMA product
 with its three epilogues against numpy, RMSNorm + residual, RoPE + K/V cache
 write (slot placement bit-exact), greedy sampling / advance.
-Model level: prefill and batched decode of small configs and of the TinyLlama
-1.1B shape against the float32 oracle (logits <= 2e-2 max-abs, the fp16 bar),
+Model level: prefill and batched decode of small configs (fp16 and fp32, the
+reference's default model dtype) and of the TinyLlama 1.1B shape against the
+float32 oracle (logits <= 2e-2 max-abs for fp16, 1e-4 for fp32),
 the reference's K/V order, graph replay vs eager launches (bit-identical, the
 reference's determinism test, test_jit_decode.py:138-171), and the
 device-resident multi-step loop.
@@ -48,7 +49,7 @@ def f64(t):
 
 # ---- linear -----------------------------------------------------------------------------
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M,N,K,ks", [(1, 64, 32, 32), (5, 100, 96, 32), (64, 2560, 2048, 256),
                                       (70, 132, 320, 64), (130, 64, 512, 512), (64, 2048, 5632, 768),
                                       (3, 40, 800, 800),
@@ -85,7 +86,7 @@ def test_linear_strided_a(K, lda, ks):
     assert np.abs(part.sum(0).double().cpu().numpy() - want).max() < 1e-4 * max(1.0, np.abs(want).max())
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("M,H,K", [(4, 48, 64), (64, 5632, 2048), (65, 96, 256), (16, 40, 4096)])
 def test_linear_swiglu(dtype, M, H, K):
     from tinyvllm_amd._lib import dtype_code
@@ -99,18 +100,21 @@ def test_linear_swiglu(dtype, M, H, K):
     torch.cuda.synchronize()
     g, u = f64(a) @ f64(w1).T, f64(a) @ f64(w3).T
     want = g / (1 + np.exp(-g)) * u
-    assert np.abs(out.double().cpu().numpy() - want).max() < TOL * max(1.0, np.abs(want).max())
+    tol = 1e-5 if dtype == torch.float32 else TOL
+    assert np.abs(out.double().cpu().numpy() - want).max() < tol * max(1.0, np.abs(want).max())
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("M,N,K", [(3, 100, 64), (64, 32000, 2048), (70, 260, 96), (70, 260, 768)])
-def test_linear_logits_and_greedy(M, N, K):
-    from tinyvllm_amd._lib import TV_F16
-    a = gen(8, M, K)
-    w = gen(9, N, K, scale=0.05)
+def test_linear_logits_and_greedy(M, N, K, dtype):
+    from tinyvllm_amd._lib import dtype_code
+    a = gen(8, M, K, dtype=dtype)
+    w = gen(9, N, K, dtype=dtype, scale=0.05)
     logits = torch.empty((M, N), dtype=torch.float32, device="cuda")
     nparts = -(-N // 64)
     keys = torch.zeros((nparts, M), dtype=torch.int64, device="cuda")
-    check(lib().tv_linear(ptr(logits), ptr(a), ptr(w), M, N, K, K, N, K, 2, ptr(keys), TV_F16, None), "logits")
+    check(lib().tv_linear(ptr(logits), ptr(a), ptr(w), M, N, K, K, N, K, 2, ptr(keys), dtype_code(dtype), None),
+          "logits")
     toks = torch.zeros(M, dtype=torch.int32, device="cuda")
     check(lib().tv_argmax_advance(ptr(toks), None, None, None, 0, ptr(keys), nparts, M, None), "argmax")
     torch.cuda.synchronize()
@@ -161,30 +165,32 @@ def test_argmax_advance_updates_state():
 
 # ---- norm / rope --------------------------------------------------------------------------
 
-def test_rms_norm_residual_embed_and_add():
-    from tinyvllm_amd._lib import TV_F16
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_rms_norm_residual_embed_and_add(dtype):
+    from tinyvllm_amd._lib import dtype_code
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
     M, dim, V = 6, 256, 50
-    emb = gen(12, V, dim)
+    emb = gen(12, V, dim, dtype=dtype)
     w = gen(13, dim, dtype=torch.float32, scale=0.3) + 1
     toks = torch.tensor([0, 7, 49, 3, 3, 22], dtype=torch.int32, device="cuda")
     x = torch.empty((M, dim), dtype=torch.float32, device="cuda")
-    xh = torch.empty((M, dim), dtype=torch.float16, device="cuda")
+    xh = torch.empty((M, dim), dtype=dtype, device="cuda")
     check(lib().tv_rms_norm_residual(ptr(x), ptr(xh), None, 0, ptr(emb), ptr(toks), V, ptr(w), M, dim, 1e-5,
-                                     TV_F16, None), "embed")
+                                     dtype_code(dtype), None), "embed")
     torch.cuda.synchronize()
     X = emb.float().cpu().numpy()[toks.cpu().numpy()]
     assert np.array_equal(x.cpu().numpy(), X)
     want = rms_norm_ref(X, w.cpu().numpy())
-    assert np.abs(xh.float().cpu().numpy() - want).max() < 2e-3 * np.abs(want).max()
+    assert np.abs(xh.float().cpu().numpy() - want).max() < tol * np.abs(want).max()
     part = gen(14, 3, M, dim, dtype=torch.float32)
     check(lib().tv_rms_norm_residual(ptr(x), ptr(xh), ptr(part), 3, None, None, 0, ptr(w), M, dim, 1e-5,
-                                     TV_F16, None), "residual")
+                                     dtype_code(dtype), None), "residual")
     torch.cuda.synchronize()
     P = part.cpu().numpy()
     X2 = ((X + P[0]) + P[1]) + P[2]
     assert np.abs(x.cpu().numpy() - X2).max() < 1e-6
     want = rms_norm_ref(X2, w.cpu().numpy())
-    assert np.abs(xh.float().cpu().numpy() - want).max() < 2e-3 * np.abs(want).max()
+    assert np.abs(xh.float().cpu().numpy() - want).max() < tol * np.abs(want).max()
 
 
 def test_rope_table_matches_oracle():
@@ -204,9 +210,11 @@ def test_rope_table_matches_oracle():
     assert np.all(np.abs(cos - np.cos(ang)) <= bound) and np.all(np.abs(sin - np.sin(ang)) <= bound)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("write_cache", [True, False])
-def test_qkv_rope_cache(write_cache):
-    from tinyvllm_amd._lib import TV_F16
+def test_qkv_rope_cache(write_cache, dtype):
+    from tinyvllm_amd._lib import dtype_code
+    tol = 1e-5 if dtype == torch.float32 else 4e-3
     M, Hq, Hkv, D, bs, NB, splits = 5, 4, 2, 32, 4, 12, 3
     N = (Hq + 2 * Hkv) * D
     part = gen(15, splits, M, N, dtype=torch.float32)
@@ -216,16 +224,17 @@ def test_qkv_rope_cache(write_cache):
     bt_np = np.array([[5, 1, 0, 0], [2, 0, 0, 0], [7, 9, 11, 0], [3, 4, 6, 8], [10, 0, 0, 0]], dtype=np.int32)
     bt_np[1, 0] = 99                          # row 1's block is outside the cache: not written, counted
     bt = torch.from_numpy(bt_np).cuda()        # row 4's position 40 is past its table (4 blocks of 4): counted
-    q = torch.empty((M, Hq * D), dtype=torch.float16, device="cuda")
-    ko = torch.empty((M, Hkv * D), dtype=torch.float16, device="cuda")
+    q = torch.empty((M, Hq * D), dtype=dtype, device="cuda")
+    ko = torch.empty((M, Hkv * D), dtype=dtype, device="cuda")
     vo = torch.empty_like(ko)
-    kc = torch.zeros((NB, bs, Hkv, D), dtype=torch.float16, device="cuda")
+    kc = torch.zeros((NB, bs, Hkv, D), dtype=dtype, device="cuda")
     vc = torch.zeros_like(kc)
     slots = torch.full((M,), 123, dtype=torch.int32, device="cuda")
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     check(lib().tv_qkv_rope_cache(ptr(q), ptr(ko), ptr(vo), ptr(kc) if write_cache else None,
                                   ptr(vc) if write_cache else None, ptr(part), splits, ptr(pos), 0, ptr(rope), 64,
-                                  ptr(bt), 4, 4, bs, NB, M, Hq, Hkv, D, TV_F16, ptr(slots), ptr(err), None), "qkv")
+                                  ptr(bt), 4, 4, bs, NB, M, Hq, Hkv, D, dtype_code(dtype), ptr(slots), ptr(err),
+                                  None), "qkv")
     torch.cuda.synchronize()
     S = part.cpu().numpy().sum(0)
     P = pos.cpu().numpy()
@@ -234,9 +243,9 @@ def test_qkv_rope_cache(write_cache):
     wq = apply_rope_ref(S[:, :Hq * D].reshape(M, Hq, D), c, s)
     wk = apply_rope_ref(S[:, Hq * D:(Hq + Hkv) * D].reshape(M, Hkv, D), c, s)
     wv = S[:, (Hq + Hkv) * D:].reshape(M, Hkv, D)
-    assert np.abs(q.float().cpu().numpy().reshape(M, Hq, D) - wq).max() < 4e-3 * np.abs(wq).max()
-    assert np.abs(ko.float().cpu().numpy().reshape(M, Hkv, D) - wk).max() < 4e-3 * np.abs(wk).max()
-    assert np.abs(vo.float().cpu().numpy().reshape(M, Hkv, D) - wv).max() < 4e-3 * np.abs(wv).max()
+    assert np.abs(q.float().cpu().numpy().reshape(M, Hq, D) - wq).max() < tol * np.abs(wq).max()
+    assert np.abs(ko.float().cpu().numpy().reshape(M, Hkv, D) - wk).max() < tol * np.abs(wk).max()
+    assert np.abs(vo.float().cpu().numpy().reshape(M, Hkv, D) - wv).max() < tol * np.abs(wv).max()
     want_slots = [5 * 4 + 0, -1, 11 * 4 + 1, 8 * 4 + 2, -1]
     assert slots.cpu().tolist() == want_slots and err.item() == 2
     K, Vc = kc.cpu().numpy().reshape(NB * bs, Hkv, D), vc.cpu().numpy().reshape(NB * bs, Hkv, D)
@@ -280,7 +289,7 @@ def build(cfg, seed=0, std=0.05, write_before_attend=True, num_blocks=64, block_
     model = Llama(cfg, weights, write_before_attend=write_before_attend)
     kv = KVCache(cfg.n_layers, num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
     bm = BlockManager(1, num_blocks, block_size)
-    ref = LlamaRef(cfg, numpy_weights(weights), cache_dtype=np.float16)
+    ref = LlamaRef(cfg, numpy_weights(weights), cache_dtype=np.float32 if cfg.dtype == torch.float32 else np.float16)
     shape = (num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim)
     rk = [np.zeros(shape, np.float32) for _ in range(cfg.n_layers)]
     rv = [np.zeros(shape, np.float32) for _ in range(cfg.n_layers)]
@@ -292,16 +301,24 @@ def max_err(got, want):
 
 
 def check_caches(kv, rk, rv):
-    """fp16 caches vs the oracle's: a few fp16 ulps of the largest entry (layer-0
-    rounding differences propagate into the later layers' k/v)."""
+    """Caches vs the oracle's: a few fp16 ulps of the largest entry for fp16
+    (layer-0 rounding differences propagate into the later layers' k/v), the
+    fp32 bar of 1e-4 relative for fp32 (summation order differs from numpy's)."""
+    rel = 1e-4 if kv.dtype == torch.float32 else 4e-3
     for layer, (k, v) in enumerate(zip(rk, rv)):
         for got, want in ((kv.k_cache[layer], k), (kv.v_cache[layer], v)):
-            bound = 4e-3 * max(1.0, float(np.abs(want).max()))
+            bound = rel * max(1.0, float(np.abs(want).max()))
             assert max_err(got.float().cpu().numpy(), want) < bound, layer
 
 
-def test_prefill_matches_oracle():
-    cfg = small_config()
+# fp16 logits within 2e-2 of the float32 oracle (the fp16 bar); fp32 models (the
+# reference's default dtype, weights.py:32) within 1e-4
+LOGIT_TOL = {"float16": TOL, "float32": 1e-4}
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_prefill_matches_oracle(dtype):
+    cfg = small_config(dtype=dtype)
     model, kv, bm, ref, rk, rv = build(cfg)
     rng = np.random.default_rng(20)
     for sid, n in enumerate([5, 17, 33]):
@@ -309,7 +326,7 @@ def test_prefill_matches_oracle():
         toks = rng.integers(0, cfg.vocab_size, n)
         logits = model.prefill(toks, kv, bm, sid)[0].cpu().numpy()
         want = ref.prefill(toks, rk, rv, np.array(bm.get_block_table(sid)), 0, 16)
-        assert max_err(logits, want) < TOL, sid
+        assert max_err(logits, want) < LOGIT_TOL[dtype], sid
         assert bm.get_context_length(sid) == n
     check_caches(kv, rk, rv)
 
@@ -332,14 +349,16 @@ def prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg):
 DECODE_SHAPES = [(128, 4, 2), (256, 4, 2), (512, 8, 1), (1024, 16, 1), (256, 2, 1)]
 
 
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
 @pytest.mark.parametrize("shape", DECODE_SHAPES, ids=lambda s: f"dim{s[0]}-h{s[1]}-kv{s[2]}")
 @pytest.mark.parametrize("write_before_attend", [True, False])
-def test_decode_steps_match_oracle(write_before_attend, shape):
+def test_decode_steps_match_oracle(write_before_attend, shape, dtype):
     """Engine convention (context = position + 1, engine.py:251) over several steps,
     teacher-forced with the oracle's greedy tokens; one context spans every wave
-    of the fused kernel."""
+    of the fused kernel (16-bit models; fp32 models take qkv_rope +
+    tv_paged_decode)."""
     dim, nh, nkv = shape
-    cfg = small_config(dim=dim, n_heads=nh, n_kv_heads=nkv, max_seq_len=512)
+    cfg = small_config(dim=dim, n_heads=nh, n_kv_heads=nkv, max_seq_len=512, dtype=dtype)
     model, kv, bm, ref, rk, rv = build(cfg, seed=3, write_before_attend=write_before_attend)
     rng = np.random.default_rng(21)
     lens = [7, 16, 300, 1]
@@ -359,14 +378,15 @@ def test_decode_steps_match_oracle(write_before_attend, shape):
                               torch.from_numpy(bt), torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
         want = ref.decode(toks, pos, ctx, bt, rk, rv, 16, write_before_attend=write_before_attend)
         assert logits.shape == (len(lens), 1, cfg.vocab_size)
-        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        assert max_err(logits[:, 0].cpu().numpy(), want) < LOGIT_TOL[dtype], step
         toks = [int(t) for t in greedy_ref(want)]
     check_caches(kv, rk, rv)
 
 
-def test_graph_replay_is_deterministic_and_equals_eager():
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_graph_replay_is_deterministic_and_equals_eager(dtype):
     from tinyvllm_amd.llama import DecodeGraph
-    cfg = small_config(n_layers=3)
+    cfg = small_config(n_layers=3, dtype=dtype)
     model, kv, bm, ref, rk, rv = build(cfg, seed=5)
     rng = np.random.default_rng(22)
     toks = prefill_batch(model, kv, bm, ref, rk, rv, [9, 12, 20], rng, cfg)

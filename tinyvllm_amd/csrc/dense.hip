@@ -10,8 +10,9 @@
 // linear_kernel computes Y = A W^T for a skinny A (the decode batch, M <= 64
 // per work-group) against a weight matrix W [N, K] that is streamed from HBM
 // exactly once.  Each of the 4 waves of a work-group owns 16 rows of W and all
-// 64 rows of A; A is staged in LDS per 256-wide K chunk and shared by the
-// waves.  W rows are the MFMA A operand (lane = output feature), A^T the B
+// 64 rows of A; A is staged in LDS per 512-byte-wide K chunk (256 fp16/bf16 or
+// 128 fp32 elements) and shared by the waves.  fp32 runs the same byte layout
+// on v_mfma_f32_16x16x4_f32, four of them per 16-byte fragment pair.  W rows are the MFMA A operand (lane = output feature), A^T the B
 // operand (lane = token), so a lane ends up holding 4 consecutive output
 // features of one token: the layout the fused epilogues want.
 #include "tv_common.h"
@@ -32,6 +33,44 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Two / four consecutive elements of T to and from floats.
+template <typename T> __device__ __forceinline__ void store2(void* base, size_t idx, float a, float b) {
+  *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(base) + idx) = pack2<T>(a, b);
+}
+template <> __device__ __forceinline__ void store2<float>(void* base, size_t idx, float a, float b) {
+  *reinterpret_cast<float2*>(reinterpret_cast<float*>(base) + idx) = float2{a, b};
+}
+template <typename T> __device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v) {
+  *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(base) + idx) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+}
+template <> __device__ __forceinline__ void store4<float>(void* base, size_t idx, f32x4 v) {
+  *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(base) + idx) = v;
+}
+template <typename T> __device__ __forceinline__ f32x4 load4(const void* base, size_t idx) {
+  const u32x2 e = *reinterpret_cast<const u32x2*>(reinterpret_cast<const T*>(base) + idx);
+  float a, b, c, d;
+  unpack2<T>(e[0], a, b);
+  unpack2<T>(e[1], c, d);
+  return f32x4{a, b, c, d};
+}
+template <> __device__ __forceinline__ f32x4 load4<float>(const void* base, size_t idx) {
+  return *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + idx);
+}
+
+// acc += (16 rows of W) x (16 columns of A^T) over the k range of one pair of
+// 16-byte fragments: one v_mfma_f32_16x16x32 for 16-bit T; for fp32 four
+// v_mfma_f32_16x16x4_f32, step j taking element j of every lane's fragment
+// (lane group g then holds k = 4 g + j in both operands, so the steps cover
+// the fragment's 16 k once).
+template <typename T> __device__ __forceinline__ f32x4 mfma_frag(u32x4 a, u32x4 b, f32x4 c) {
+  return mfma16x16x32<T>(a, b, c);
+}
+template <> __device__ __forceinline__ f32x4 mfma_frag<float>(u32x4 a, u32x4 b, f32x4 c) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(u32_as_f32(a[j]), u32_as_f32(b[j]), c, 0, 0, 0);
+  return c;
+}
 
 #ifndef TV_LINEAR_MIN_BLOCKS
 #define TV_LINEAR_MIN_BLOCKS 1
@@ -73,8 +112,7 @@ __device__ __forceinline__ void linear_epilogue(const LinearParams& p, const f32
       const int m = m0 + mb * 16 + col;
       if (m < p.M && n < p.N) {
         const f32x4 v = acc[mb];
-        const uint32_t h = pack2<T>(silu(v[0]) * v[2], silu(v[1]) * v[3]);
-        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)m * p.ldo + (n >> 1)) = h;
+        store2<T>(p.out, (size_t)m * p.ldo + (n >> 1), silu(v[0]) * v[2], silu(v[1]) * v[3]);
       }
     }
   } else {
@@ -103,7 +141,11 @@ __device__ __forceinline__ void linear_epilogue(const LinearParams& p, const f32
 
 template <typename T, int EPI>
 __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const LinearParams p) {
-  constexpr int KP = kLinKC + 16;  // LDS pitch: 544 bytes, an odd multiple of 32 modulo 256 -- conflict-free 16-byte reads
+  // LDS in 16-bit units; a chunk row is 512 bytes of K at a 544-byte pitch (an
+  // odd multiple of 32 modulo 256: conflict-free 16-byte reads)
+  constexpr int KP = 256 + 16;
+  constexpr int KC = 512 / (int)sizeof(T);   // K elements per chunk
+  constexpr int VE = 16 / (int)sizeof(T);    // K elements per 16-byte vector
   __shared__ __attribute__((aligned(16))) uint16_t sa[2][kLinBM * KP];   // A chunk, double-buffered
 
   const int tid = threadIdx.x;
@@ -122,7 +164,7 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
   const int m0 = blockIdx.z * kLinBM;
   const int kb = split * p.k_split;
   const int ke = min(kb + p.k_split, p.K);
-  const int nc = (ke - kb + kLinKC - 1) / kLinKC;
+  const int nc = (ke - kb + KC - 1) / KC;
   const int rot = ntile % nc;
   auto chunk_of = [&](int i) { const int c = i + rot; return c < nc ? c : c - nc; };
 
@@ -135,27 +177,27 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
                                                 (unsigned long long)w_rows * p.K * sizeof(T));
   const __amdgpu_buffer_rsrc_t ares = make_rsrc(reinterpret_cast<const T*>(p.a) + (size_t)m0 * p.lda,
                                                 (unsigned long long)max(p.M - m0, 0) * p.lda * sizeof(T));
-  const int w_voff = (col * p.K + kb + 8 * g) * (int)sizeof(T);
-  const int a_voff = ((tid >> 5) * (int)p.lda + kb + 8 * (tid & 31)) * (int)sizeof(T);
+  const int w_voff = (col * p.K + kb) * (int)sizeof(T) + 16 * g;
+  const int a_voff = ((tid >> 5) * (int)p.lda + kb) * (int)sizeof(T) + 16 * (tid & 31);
   const int a_rows8 = 8 * (int)p.lda * (int)sizeof(T);   // byte step between the 8 rows a thread loads
 
-  // W: lane (row col, k group g) reads 8 elements per 32-wide k step.  Columns
+  // W: lane (row col, k group g) reads 16 bytes per 64-byte k step.  Columns
   // past the split are multiplied by zero rows of A.
   // i is the position in this work-group's chunk sequence; positions past the
   // last chunk re-read it (W) or load zeros (A), so padding steps add nothing.
   auto loadW = [&](int i, u32x4 (&r)[8]) {
-    const int off = w_voff + chunk_of(min(i, nc - 1)) * kLinKC * (int)sizeof(T);
+    const int off = w_voff + chunk_of(min(i, nc - 1)) * 512;
 #pragma unroll
     for (int s = 0; s < 8; ++s) r[s] = buffer_load16(wres, off + 64 * s, 0);
   };
-  // A chunk: 64 rows x 32 vectors of 8 elements; thread tid loads vector
+  // A chunk: 64 rows x 32 vectors of 16 bytes; thread tid loads vector
   // tid % 32 of rows tid / 32 + 8 i.  Columns past the split are zeroed when
   // stored to LDS (not at load time, so the loads stay in flight while the
   // previous chunk computes).
   auto loadA = [&](int i, u32x4 (&r)[8], bool& valid) {
     const int c = chunk_of(min(i, nc - 1));
-    valid = i < nc && kb + c * kLinKC + 8 * (tid & 31) < ke;
-    const int off = a_voff + c * kLinKC * (int)sizeof(T);
+    valid = i < nc && kb + c * KC + VE * (tid & 31) < ke;
+    const int off = a_voff + c * 512;
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = buffer_load16(ares, off + i * a_rows8, 0);   // row in the range-checked offset
   };
@@ -182,7 +224,7 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
           b[(s + 1) & 1][mb] = *reinterpret_cast<const u32x4*>(&sa[buf][(mb * 16 + col) * KP + 32 * (s + 1) + 8 * g]);
       }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma16x16x32<T>(r[s], b[s & 1][mb], acc[mb]);
+      for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma_frag<T>(r[s], b[s & 1][mb], acc[mb]);
     }
   };
 
@@ -242,8 +284,10 @@ void launch_linear(const LinearParams& p, int epi, int dtype, hipStream_t s) {
   const dim3 grid((p.K + p.k_split - 1) / p.k_split, (p.N + kLinBN - 1) / kLinBN, (p.M + kLinBM - 1) / kLinBM);
   if (dtype == kF16) {
     TV_LINEAR_CASE(_Float16)
-  } else {
+  } else if (dtype == kBF16) {
     TV_LINEAR_CASE(__bf16)
+  } else {
+    TV_LINEAR_CASE(float)
   }
 }
 
@@ -269,11 +313,7 @@ __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
     const int k = min(4 * (threadIdx.x + 256 * i), p.dim - 4);   // clamped: lanes past dim re-read the last vector
     w[i] = *reinterpret_cast<const f32x4*>(p.weight + k);
     if (p.emb) {
-      const u32x2 e = *reinterpret_cast<const u32x2*>(reinterpret_cast<const T*>(p.emb) + (size_t)tok * p.dim + k);
-      float e0, e1, e2, e3;
-      unpack2<T>(e[0], e0, e1);
-      unpack2<T>(e[1], e2, e3);
-      v[i] = f32x4{e0, e1, e2, e3};
+      v[i] = load4<T>(p.emb, (size_t)tok * p.dim + k);
     } else {
       v[i] = *reinterpret_cast<const f32x4*>(x + k);
     }
@@ -314,9 +354,7 @@ __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
   for (int i = 0; i < VPT; ++i) {
     const int k = 4 * (threadIdx.x + 256 * i);
     if (k < p.dim) {
-      const f32x4 a = v[i] * r * w[i];
-      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.xh) + (size_t)m * p.dim + k) =
-          u32x2{pack2<T>(a[0], a[1]), pack2<T>(a[2], a[3])};
+      store4<T>(p.xh, (size_t)m * p.dim + k, v[i] * r * w[i]);
     }
   }
 }
@@ -332,8 +370,10 @@ template <typename T> void launch_norm_t(const NormParams& p, hipStream_t s) {
 void launch_norm(const NormParams& p, int dtype, hipStream_t s) {
   if (dtype == kF16)
     launch_norm_t<_Float16>(p, s);
-  else
+  else if (dtype == kBF16)
     launch_norm_t<__bf16>(p, s);
+  else
+    launch_norm_t<float>(p, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -366,15 +406,14 @@ __global__ void __launch_bounds__(256) qkv_rope_kernel(const QKVParams p) {
     v0 = a;
     v1 = b;
   }
-  const uint32_t packed = pack2<T>(v0, v1);
   if (n < qn) {
-    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.q) + (size_t)m * qn + n) = packed;
+    store2<T>(p.q, (size_t)m * qn + n, v0, v1);
     return;
   }
   const bool is_k = n < qn + kn;
   const int e = is_k ? n - qn : n - qn - kn;
   void* stage = is_k ? p.k_out : p.v_out;
-  if (stage) *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(stage) + (size_t)m * kn + e) = packed;
+  if (stage) store2<T>(stage, (size_t)m * kn + e, v0, v1);
   void* cache = is_k ? p.k_cache : p.v_cache;
   const bool report = is_k && e == 0;   // one thread per row reports the slot
   if (!p.block_tables || (!cache && !(report && (p.slots || p.err_count)))) return;
@@ -383,8 +422,7 @@ __global__ void __launch_bounds__(256) qkv_rope_kernel(const QKVParams p) {
     const int blk = p.block_tables[(size_t)m * p.bt_row_step + pos / p.block_size];
     if (blk >= 0 && blk < p.num_blocks) slot = (long long)blk * p.block_size + pos % p.block_size;
   }
-  if (cache && slot >= 0)
-    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(cache) + (size_t)slot * kn + e) = packed;
+  if (cache && slot >= 0) store2<T>(cache, (size_t)slot * kn + e, v0, v1);
   if (report) {
     if (p.slots) p.slots[m] = (int)slot;
     if (slot < 0 && p.err_count) atomicAdd(p.err_count, 1u);
@@ -396,8 +434,10 @@ void launch_qkv_rope(const QKVParams& p, int dtype, hipStream_t s) {
   const dim3 grid((unsigned)((pairs + 255) / 256));
   if (dtype == kF16)
     hipLaunchKernelGGL(qkv_rope_kernel<_Float16>, grid, dim3(256), 0, s, p);
-  else
+  else if (dtype == kBF16)
     hipLaunchKernelGGL(qkv_rope_kernel<__bf16>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(qkv_rope_kernel<float>, grid, dim3(256), 0, s, p);
 }
 
 __global__ void rope_table_kernel(float* table, int max_pos, int head_dim, float theta) {

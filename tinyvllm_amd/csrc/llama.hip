@@ -30,7 +30,8 @@ using tv::ok;
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 long long round_up(long long x, long long a) { return (x + a - 1) / a * a; }
 
-bool mfma_dtype(int d) { return d == TV_F16 || d == TV_BF16; }
+bool step_dtype(int d) { return d == TV_F16 || d == TV_BF16 || d == TV_F32; }
+size_t elem_bytes(int d) { return d == TV_F32 ? 4 : 2; }
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int splits_of(int K, int k_split) { return (K + k_split - 1) / k_split; }
@@ -52,7 +53,7 @@ struct StepLayout {
 
 int validate_model(const tv_llama_model* m, const char* who) {
   if (!m) return fail(TV_EINVAL, "%s: null model", who);
-  if (!mfma_dtype(m->dtype)) return fail(TV_EUNSUPPORTED, "%s: dtype %d (float16 / bfloat16 only)", who, m->dtype);
+  if (!step_dtype(m->dtype)) return fail(TV_EUNSUPPORTED, "%s: dtype %d (float32 / float16 / bfloat16)", who, m->dtype);
   if (m->n_layers <= 0 || m->dim <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 || m->head_dim <= 0 ||
       m->hidden_dim <= 0 || m->vocab_size <= 0 || m->n_heads % m->n_kv_heads != 0)
     return fail(TV_EINVAL, "%s: bad model shape", who);
@@ -83,7 +84,7 @@ StepLayout step_layout(const tv_llama_model* m, int B, int max_blocks, int block
   L.ks_2 = tv_linear_k_split(B, m->dim, m->hidden_dim);
   const size_t part_floats = std::max({(size_t)splits_of(m->dim, L.ks_qkv) * nqkv, (size_t)splits_of(qd, L.ks_o) * m->dim,
                                        (size_t)splits_of(m->hidden_dim, L.ks_2) * m->dim}) * (size_t)B;
-  const size_t es = 2;
+  const size_t es = elem_bytes(m->dtype);
   Carver c;
   L.part = c.take(part_floats * 4);
   L.q = c.take((size_t)B * qd * es);
@@ -269,8 +270,9 @@ int run_layers(const tv_llama_model* m, const tv_llama_cache* c, const LayerIO& 
   const int qd = m->n_heads * m->head_dim;
   const int nqkv = qkv_width(m);
   const int M = io.M;
-  const bool fused_attn =
-      io.decode && tv::step_attn_supported(m->head_dim, m->n_heads / m->n_kv_heads, c->block_size);
+  // the fused step attention runs on 16-bit MFMA; fp32 models take qkv_rope + tv_paged_decode
+  const bool fused_attn = io.decode && dt != TV_F32 &&
+                          tv::step_attn_supported(m->head_dim, m->n_heads / m->n_kv_heads, c->block_size);
   for (int l = 0; l < m->n_layers; ++l) {
     linear(io.xh, m->wqkv[l], M, nqkv, m->dim, m->dim, io.ks_qkv, tv::kEpiPartial, io.part, 0, nullptr, dt, s);
     int rc = fused_attn ? attend_fused(m, c, io, l, s) : attend_unfused(m, c, io, l, s);
@@ -319,7 +321,7 @@ int tv_linear_k_split(int M, int N, int K) {
 int tv_linear(void* out, const void* a, const void* w, int M, int N, int K, int64_t lda, int64_t ldo, int k_split,
               int epilogue, uint64_t* keys, int dtype, void* stream) {
   if (!a || !w || (!out && epilogue != TV_EPI_LOGITS)) return fail(TV_EINVAL, "tv_linear: null pointer argument");
-  if (!mfma_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_linear: dtype %d (float16 / bfloat16 only)", dtype);
+  if (!step_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_linear: dtype %d (float32 / float16 / bfloat16)", dtype);
   if (M <= 0 || N <= 0 || K <= 0) return fail(TV_EINVAL, "tv_linear: bad shape %d x %d x %d", M, N, K);
   if (K % 32 || N % 4) return fail(TV_EUNSUPPORTED, "tv_linear: K %% 32 and N %% 4 must be 0 (K=%d, N=%d)", K, N);
   if (lda < K) return fail(TV_EINVAL, "tv_linear: lda %lld < K %d", (long long)lda, K);
@@ -344,7 +346,7 @@ int tv_linear(void* out, const void* a, const void* w, int M, int N, int K, int6
 int tv_rms_norm_residual(float* x, void* xh, const float* part, int splits, const void* emb, const int32_t* tokens,
                          int vocab, const float* weight, int M, int dim, float eps, int dtype, void* stream) {
   if (!x || !xh || !weight || (emb && !tokens)) return fail(TV_EINVAL, "tv_rms_norm_residual: null pointer argument");
-  if (!mfma_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_rms_norm_residual: dtype %d (float16 / bfloat16 only)", dtype);
+  if (!step_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_rms_norm_residual: dtype %d (float32 / float16 / bfloat16)", dtype);
   if (M <= 0 || dim <= 0 || dim % 4 || (part && splits <= 0) || (emb && vocab <= 0))
     return fail(TV_EINVAL, "tv_rms_norm_residual: bad shape (M=%d, dim=%d, splits=%d)", M, dim, splits);
   if (dim > 8192) return fail(TV_EUNSUPPORTED, "tv_rms_norm_residual: dim %d above 8192", dim);
@@ -369,7 +371,7 @@ int tv_qkv_rope_cache(void* q, void* k_out, void* v_out, void* k_cache, void* v_
                       int M, int n_heads, int n_kv_heads, int head_dim, int dtype, int32_t* slots,
                       uint32_t* err_count, void* stream) {
   if (!q || !part || !rope) return fail(TV_EINVAL, "tv_qkv_rope_cache: null pointer argument");
-  if (!mfma_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_qkv_rope_cache: dtype %d (float16 / bfloat16 only)", dtype);
+  if (!step_dtype(dtype)) return fail(TV_EUNSUPPORTED, "tv_qkv_rope_cache: dtype %d (float32 / float16 / bfloat16)", dtype);
   if (M <= 0 || splits <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 || rope_len <= 0)
     return fail(TV_EINVAL, "tv_qkv_rope_cache: bad shape");
   if (!k_cache != !v_cache) return fail(TV_EINVAL, "tv_qkv_rope_cache: give both caches or neither");
@@ -566,7 +568,7 @@ int tv_llama_prefill(const tv_llama_model* m, const tv_llama_cache* c, const tv_
   rc = run_layers(m, c, io, s);
   if (rc != TV_OK) return rc;
   unsigned long long* keys = at<unsigned long long>(ws, L.keys);
-  const size_t es = 2;
+  const size_t es = elem_bytes(m->dtype);
   const void* last = reinterpret_cast<const char*>(io.xh) + (size_t)(M - 1) * m->dim * es;
   if (a->logits) {
     if (a->logits_last_only)

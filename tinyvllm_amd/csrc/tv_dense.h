@@ -10,7 +10,7 @@ enum LinearEpilogue : int { kEpiPartial = 0, kEpiSwiglu = 1, kEpiLogits = 2 };
 
 constexpr int kLinBM = 64;    // rows of A (tokens) per work-group
 constexpr int kLinBN = 64;    // rows of W (output features) per work-group, 16 per wave
-constexpr int kLinKC = 256;   // K elements staged in LDS per chunk
+constexpr int kLinKC = 256;   // K elements per LDS chunk at 16-bit types (512 bytes; 128 at fp32)
 
 // Y = A W^T over the K range of one split; grid (splits, ceil(N/64), ceil(M/64)).
 struct LinearParams {

@@ -14,8 +14,10 @@ Mirrors tinyvllm/model/llama.py:347-453 and tinyvllm/model/weights.py:17-58:
 * ``Llama.load_weights``     -- llama.py:390-445 (Meta- and HF-style names)
 
 Every forward operation runs in HIP kernels behind include/tv_llama.h; PyTorch
-only owns buffers and copies inputs into them.  The products run on MFMA, so
-the model dtype must be float16 or bfloat16.
+only owns buffers and copies inputs into them.  The model dtype is float32
+(the reference's default), float16 or bfloat16; the products run on MFMA in all
+three, and fp32 decode attention takes the separate RoPE and paged-decode
+kernels (the fused step attention is 16-bit only).
 
 K/V order: the reference attends first and writes the step's K/V afterwards
 (llama.py:378-386), so with the engine's ``context_len = position + 1``
@@ -187,8 +189,8 @@ class Llama:
     """LLaMA model on the HIP decode step (llama.py:347-453)."""
 
     def __init__(self, config, weights=None, *, seed=0, write_before_attend=True, device="cuda"):
-        if config.dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError("the MI355X step runs its products on MFMA: dtype must be float16 or bfloat16")
+        if config.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise ValueError("model dtype must be float32, float16 or bfloat16")
         if config.n_heads % config.n_kv_heads or config.hidden_dim % 2:
             raise ValueError("n_heads must be a multiple of n_kv_heads and hidden_dim even")
         self.config = config
