@@ -119,6 +119,26 @@ int tv_flash_prefill(void* out, const void* q, const void* k, const void* v,
                      int chunk_tiles, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Several prompts in one launch.  No counterpart in the reference, whose engine
+ * prefills one sequence per call (engine.py:125-132, llama.py:65-67 asserts
+ * batch 1); each prompt is attended exactly as tv_flash_prefill attends it.
+ * Prompt z owns rows cu_seqlens_q[z] .. cu_seqlens_q[z+1] of q / out and rows
+ * cu_seqlens_k[z] .. cu_seqlens_k[z+1] of k / v (device int32 arrays of
+ * num_seqs + 1 entries).  seq_order (device int32 [num_seqs], may be NULL) is
+ * the order in which prompts are dispatched -- longest first balances the
+ * launch.  max_q_len / max_kv_len must bound every prompt's lengths (rows past
+ * max_q_len are not computed); total_q is the sum of query lengths (kernel
+ * shape choice only).  fp16 / bf16, head_dim 64 or 128, 16-byte aligned rows
+ * (TV_EUNSUPPORTED otherwise); no workspace.
+ */
+int tv_flash_prefill_varlen(void* out, const void* q, const void* k, const void* v,
+                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, const int32_t* seq_order,
+                            int num_seqs, int max_q_len, int max_kv_len, int64_t total_q,
+                            int num_heads, int num_kv_heads, int head_dim,
+                            int64_t q_stride, int64_t k_stride, int64_t v_stride, int64_t out_stride,
+                            int causal, float scale, int dtype, int out_dtype, void* stream);
+
+/*
  * Fused K/V cache write from a slot mapping.  Replaces the per-chunk
  * KVCache.write_kv loop (tinyvllm/core/kv_cache.py:34-38 called from
  * llama.py:199-209 and llama.py:381-386) with one launch:

@@ -218,3 +218,70 @@ def test_random_shapes(i, hq, hkv, d, lq, lk, causal, dtype, chunk):
     torch.cuda.synchronize()
     want = flash_prefill_ref(q.float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None], causal)[0]
     assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]
+
+
+# ---- several prompts per launch (no reference counterpart) ------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("lens,hq,hkv,d,causal", [
+    ([512, 1024], 32, 4, 64, True),            # the TinyLlama prompts of the benchmark in one launch
+    ([1, 17, 64, 300, 65], 8, 2, 64, True),    # ragged, single-token and tile-boundary prompts
+    ([129, 7, 1000], 16, 8, 128, True),
+    ([33, 200, 64], 8, 8, 64, False),
+])
+def test_varlen_matches_per_prompt(lens, hq, hkv, d, causal, dtype):
+    """Every prompt of a packed batch equals the oracle on that prompt alone and
+    the single-prompt launch (each within the fp16/bf16 bar)."""
+    from tinyvllm_amd.attention import flash_prefill_varlen
+    tot = sum(lens)
+    q, k, v = randn(60, tot, hq, d, dtype=dtype), randn(61, tot, hkv, d, dtype=dtype), randn(62, tot, hkv, d, dtype=dtype)
+    out = flash_prefill_varlen(q.cuda(), k.cuda(), v.cuda(), lens, causal)
+    torch.cuda.synchronize()
+    assert out.shape == (tot, hq, d) and out.dtype == dtype
+    got = out.float().cpu().numpy()
+    s = 0
+    for n in lens:
+        sl = slice(s, s + n)
+        want = flash_prefill_ref(q[sl].float().numpy()[None], k[sl].float().numpy()[None],
+                                 v[sl].float().numpy()[None], causal)[0]
+        assert np.abs(got[sl] - want).max() <= TOL[dtype], (n, s)
+        single = flash(q[sl], k[sl], v[sl], causal).float().cpu().numpy()
+        assert np.abs(got[sl] - single).max() <= TOL[dtype], (n, s)
+        s += n
+
+
+def test_varlen_plan_replays_in_graph():
+    """The plan captured in a HIP graph: replays (with eager work between them)
+    equal the eager launch."""
+    from tinyvllm_amd.attention import VarlenPrefillPlan
+    lens = [300, 41, 512]
+    tot = sum(lens)
+    q, k, v = (randn(63 + i, tot, h, 64, dtype=torch.float16).cuda() for i, h in enumerate((8, 2, 2)))
+    plan = VarlenPrefillPlan(q, k, v, lens)
+    eager = plan.run().clone()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            plan.run()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        plan.out.zero_()
+        junk = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.out, eager)
+        del junk
+
+
+def test_varlen_rejects_bad_arguments():
+    from tinyvllm_amd.attention import flash_prefill_varlen
+    q = torch.zeros((10, 4, 64), dtype=torch.float16, device="cuda")
+    k = torch.zeros((10, 2, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        flash_prefill_varlen(q, k, k, [4, 5])                  # lengths do not sum to T
+    with pytest.raises(ValueError):
+        flash_prefill_varlen(q, k, k, [10, 0])                 # empty prompt
+    with pytest.raises(RuntimeError, match="head_dim 64 or 128"):
+        flash_prefill_varlen(q.float(), k.float(), k.float(), [10])   # fp32: MFMA path only

@@ -9,6 +9,7 @@ tensors on a HIP device; all arithmetic runs in libtvattn.so (no fallback).
 
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -137,6 +138,58 @@ def flash_prefill_attention(queries, keys, values, causal=True, *, out_dtype=Non
         ws.data_ptr() if ws is not None else None, ws_bytes, _lib.stream_ptr(dev))
     _lib.check(rc, "flash_prefill_attention")
     return out
+
+
+class VarlenPrefillPlan:
+    """Several prompts in one prefill launch (no reference counterpart: the
+    engine prefills one sequence per call, engine.py:125-132).
+
+    queries [T, Hq, D], keys / values [T, Hkv, D] (or with a leading batch
+    dimension of 1) hold the prompts back to back; ``seq_lens`` (host ints)
+    are their lengths, summing to T.  Each prompt attends within itself exactly
+    as ``flash_prefill_attention`` attends one prompt (``causal``: key j masked
+    for query i when j > i).  fp16 / bf16 with head_dim 64 or 128.  The plan
+    holds the output and the device offsets, so ``run()`` is one C call (HIP
+    graph capture works); the inputs must stay alive while it is used.
+    """
+
+    def __init__(self, queries, keys, values, seq_lens, causal=True, *, out_dtype=None):
+        self.lib = _lib.load()
+        self.dev = _on_gpu(queries, keys, values)
+        q, k, v = (t[0] if t.dim() == 4 else t for t in (queries, keys, values))
+        _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "inputs must be [T, H, D] or [1, T, H, D]")
+        for t, name in ((q, "queries"), (k, "keys"), (v, "values")):
+            _require(t.stride(2) == 1 and t.stride(1) == t.shape[2], f"{name}: heads and head_dim must be contiguous")
+        tot, hq, d = q.shape
+        _, hkv, dk = k.shape
+        _require(dk == d and tuple(v.shape) == tuple(k.shape), "keys and values must be [T, Hkv, D] with the queries' D")
+        _require(k.shape[0] == tot, "keys and values must hold the same tokens as the queries")
+        _require(hq % hkv == 0, "query heads must be a multiple of KV heads")
+        _require(q.dtype == k.dtype == v.dtype, "queries, keys and values must share a dtype")
+        lens = [int(n) for n in seq_lens]
+        _require(len(lens) > 0 and min(lens) > 0 and sum(lens) == tot, "seq_lens must be positive and sum to T")
+        cu = np.zeros(len(lens) + 1, np.int32)
+        cu[1:] = np.cumsum(lens)
+        order = np.argsort(-np.asarray(lens), kind="stable").astype(np.int32)   # longest first
+        self.cu = torch.from_numpy(cu).to(self.dev)
+        self.order = torch.from_numpy(order).to(self.dev)
+        out_dtype = q.dtype if out_dtype is None else out_dtype
+        self.out = torch.empty((tot, hq, d), dtype=out_dtype, device=self.dev)
+        self._args = (self.out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), self.cu.data_ptr(),
+                      self.cu.data_ptr(), self.order.data_ptr(), len(lens), max(lens), max(lens), tot, hq, hkv, d,
+                      q.stride(0), k.stride(0), v.stride(0), hq * d, 1 if causal else 0, 1.0 / math.sqrt(d),
+                      _lib.dtype_code(q.dtype), _lib.dtype_code(out_dtype))
+
+    def run(self):
+        rc = self.lib.tv_flash_prefill_varlen(*self._args, _lib.stream_ptr(self.dev))
+        _lib.check(rc, "flash_prefill_varlen")
+        return self.out
+
+
+def flash_prefill_varlen(queries, keys, values, seq_lens, causal=True, *, out_dtype=None):
+    """Prefill attention over several prompts in one launch; see VarlenPrefillPlan.
+    Returns [T, Hq, D]."""
+    return VarlenPrefillPlan(queries, keys, values, seq_lens, causal, out_dtype=out_dtype).run()
 
 
 class PagedDecodePlan:

@@ -144,7 +144,23 @@ template <int KB> __device__ __forceinline__ float max_tile(const f32x4 (&st)[KB
 
 template <typename T, int D, int RB, int KS, int BN>
 __global__ void __launch_bounds__(256 / RB * KS) __attribute__((amdgpu_waves_per_eu(TV_PREFILL_WAVES_PER_EU)))
-prefill_fa_kernel(const PrefillParams p) {
+prefill_fa_kernel(const PrefillParams pa) {
+  // Several prompts per launch: this work-group's prompt is seq_order[blockIdx.z];
+  // its rows become the whole problem (pointers and lengths rebased).  Chunked
+  // key splits are off then, so a query tile is one unit and units past the
+  // prompt's tiles have nothing to do.
+  PrefillParams p = pa;
+  if (pa.cu_q) {
+    const int z = pa.seq_order ? pa.seq_order[blockIdx.z] : (int)blockIdx.z;
+    const int q0 = pa.cu_q[z], k0 = pa.cu_k[z];
+    p.q_len = pa.cu_q[z + 1] - q0;
+    p.kv_len = pa.cu_k[z + 1] - k0;
+    if ((int)blockIdx.y * kPrefillBM >= p.q_len || p.kv_len <= 0) return;
+    p.q = reinterpret_cast<const T*>(pa.q) + (size_t)q0 * pa.q_stride;
+    p.k = reinterpret_cast<const T*>(pa.k) + (size_t)k0 * pa.k_stride;
+    p.v = reinterpret_cast<const T*>(pa.v) + (size_t)k0 * pa.v_stride;
+    p.out = reinterpret_cast<char*>(pa.out) + (size_t)q0 * pa.out_stride * (pa.out_dtype == kF32 ? 4 : 2);
+  }
   constexpr int QW = 4 / RB;              // waves of a group along the 64 query rows
   constexpr int GT = 64 * QW;             // threads of a group
   constexpr int BM = kPrefillBM;
@@ -679,6 +695,37 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
   if (dtype == kF32) hipLaunchKernelGGL((prefill_generic_kernel<float>), grid, dim3(64), 0, stream, p_in);
   else if (dtype == kF16) hipLaunchKernelGGL((prefill_generic_kernel<_Float16>), grid, dim3(64), 0, stream, p_in);
   else hipLaunchKernelGGL((prefill_generic_kernel<__bf16>), grid, dim3(64), 0, stream, p_in);
+  return 0;
+}
+
+// Several prompts in one launch (MFMA path only): grid (Hq, query tiles of the
+// longest prompt, prompts); the kernel shape is chosen as for one prompt of the
+// longest length with the live work-groups of all prompts.  Returns 1 if the
+// shape has no MFMA kernel.
+int launch_flash_prefill_varlen(const PrefillParams& p_in, int num_seqs, int max_q_len, int max_kv_len,
+                                long long total_q, int dtype, hipStream_t stream) {
+  PrefillParams pp = p_in;
+  pp.q_len = max_q_len;
+  pp.kv_len = max_kv_len;
+  if (!prefill_uses_mfma(pp, dtype)) return 1;
+  pp.xcd_remap = (pp.num_heads % 8 == 0) ? 1 : 0;
+  pp.chunk_tiles = 1 << 20;
+  pp.max_chunks = 1;
+  pp.part_o = nullptr;
+  pp.part_ml = nullptr;
+  const int nqt = (max_q_len + kPrefillBM - 1) / kPrefillBM;
+  const dim3 grid(pp.num_heads, nqt, num_seqs);
+  const long long wgs = (long long)pp.num_heads * ((total_q + kPrefillBM - 1) / kPrefillBM + num_seqs);
+  const bool d64 = pp.head_dim == 64;
+  const bool long_rows = prefill_key_tiles_host(pp, nqt - 1) >= 8;
+  const int cfg = long_rows && wgs <= 256 ? 0 : (d64 && long_rows && wgs < 1024 ? 2 : 1);
+  if (dtype == kF16) {
+    if (d64) launch_fa<_Float16, 64>(cfg, grid, pp, stream);
+    else launch_fa<_Float16, 128>(cfg, grid, pp, stream);
+  } else {
+    if (d64) launch_fa<__bf16, 64>(cfg, grid, pp, stream);
+    else launch_fa<__bf16, 128>(cfg, grid, pp, stream);
+  }
   return 0;
 }
 

@@ -83,7 +83,7 @@ int vec_width(std::initializer_list<long long> sizes, std::initializer_list<cons
 
 extern "C" {
 
-int tv_abi_version(void) { return 4; }
+int tv_abi_version(void) { return 5; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
@@ -301,6 +301,39 @@ int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int
     return fail(TV_EINVAL, "tv_flash_prefill: workspace of %zu bytes required (got %zu)",
                 tv::prefill_workspace_bytes(p, dtype), workspace_bytes);
   return check_launch("tv_flash_prefill");
+}
+
+int tv_flash_prefill_varlen(void* out, const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
+                            const int32_t* cu_seqlens_k, const int32_t* seq_order, int num_seqs, int max_q_len,
+                            int max_kv_len, int64_t total_q, int num_heads, int num_kv_heads, int head_dim,
+                            int64_t q_stride, int64_t k_stride, int64_t v_stride, int64_t out_stride, int causal,
+                            float scale, int dtype, int out_dtype, void* stream) {
+  if (!out || !q || !k || !v || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(TV_EINVAL, "tv_flash_prefill_varlen: null pointer argument");
+  if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
+    return fail(TV_EINVAL, "tv_flash_prefill_varlen: bad dtype %d / out_dtype %d", dtype, out_dtype);
+  if (num_seqs <= 0 || num_seqs > 65535 || max_q_len <= 0 || max_kv_len <= 0 || total_q < max_q_len)
+    return fail(TV_EINVAL, "tv_flash_prefill_varlen: bad sizes (num_seqs=%d, max_q_len=%d, max_kv_len=%d)",
+                num_seqs, max_q_len, max_kv_len);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads > 65535)
+    return fail(TV_EINVAL, "tv_flash_prefill_varlen: bad head counts (%d, %d)", num_heads, num_kv_heads);
+  if (q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim ||
+      v_stride < (int64_t)num_kv_heads * head_dim || out_stride < (int64_t)num_heads * head_dim)
+    return fail(TV_EINVAL, "tv_flash_prefill_varlen: token stride smaller than a token row");
+  if (max_q_len > 65535 * 64) return fail(TV_EINVAL, "tv_flash_prefill_varlen: grid too large");
+  tv::PrefillParams p;
+  prefill_params(p, out, q, k, v, max_q_len, max_kv_len, num_heads, num_kv_heads, head_dim, head_dim, q_stride,
+                 k_stride, v_stride, out_stride, causal, scale, out_dtype, 0);
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.seq_order = seq_order;
+  const int rc = tv::launch_flash_prefill_varlen(p, num_seqs, max_q_len, max_kv_len, total_q, dtype,
+                                                 reinterpret_cast<hipStream_t>(stream));
+  if (rc == 1)
+    return fail(TV_EUNSUPPORTED,
+                "tv_flash_prefill_varlen: fp16 / bf16, head_dim 64 or 128 and 16-byte aligned rows only "
+                "(dtype %d, head_dim %d)", dtype, head_dim);
+  return check_launch("tv_flash_prefill_varlen");
 }
 
 static int kv_write_common(const char* name, void* k_cache, void* v_cache, const void* k, const void* v,

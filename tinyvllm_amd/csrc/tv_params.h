@@ -29,6 +29,12 @@ struct PrefillParams {
   int max_chunks;        // largest number of key chunks of one query tile
   float* part_o;         // [Hq, nqt, max_chunks, 64, head_dim] chunk outputs (split tiles only)
   float* part_ml;        // [Hq, nqt, max_chunks, 64, 2] chunk (max, sum)
+  // Several prompts per launch (null: one prompt).  Prompt z's tokens are rows
+  // cu_q[z] .. cu_q[z+1] of q / out and cu_k[z] .. cu_k[z+1] of k / v; grid.z
+  // runs over seq_order (prompt ids, longest first) when it is set.
+  const int* cu_q;
+  const int* cu_k;
+  const int* seq_order;
 };
 
 // Cache write from a slot mapping or a base slot (kv_cache.hip).
@@ -64,6 +70,8 @@ bool prefill_uses_mfma(const PrefillParams& p, int dtype);
 size_t prefill_workspace_bytes(const PrefillParams& p, int dtype);
 int launch_flash_prefill(const PrefillParams& p, int dtype, void* workspace, size_t workspace_bytes,
                          hipStream_t stream);
+int launch_flash_prefill_varlen(const PrefillParams& p, int num_seqs, int max_q_len, int max_kv_len,
+                                long long total_q, int dtype, hipStream_t stream);
 void launch_kv_write(const KVWriteParams& p, int vec_bytes, hipStream_t stream);
 void launch_kv_gather(const KVGatherParams& p, int vec_bytes, hipStream_t stream);
 
