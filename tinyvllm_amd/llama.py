@@ -76,6 +76,13 @@ class LlamaConfig:
                    rope_theta=d.get("rope_theta", 10000.0), dtype=dtype)
 
     @classmethod
+    def from_json(cls, path, dtype="float32"):
+        """From a ``config.json`` / ``params.json`` file (weights.py:62-66)."""
+        import json
+        with open(path) as f:
+            return cls.from_dict(json.load(f), dtype=dtype)
+
+    @classmethod
     def tinyllama_1b(cls, dtype="float16"):
         """TinyLlama-1.1B: 22 layers, dim 2048, 32 q / 4 KV heads, MLP 5632, vocab 32000."""
         return cls(dim=2048, n_layers=22, n_heads=32, n_kv_heads=4, vocab_size=32000, hidden_dim=5632,
