@@ -76,7 +76,9 @@ int tv_paged_decode_partition_size(int num_seqs, int num_heads, int num_kv_heads
  * over positions j < min(context_lens[b], max_blocks*block_size) of sequence b,
  * where position j lives in block block_tables[b, j / block_size] at row
  * j % block_size, and query head h reads KV head h / (num_heads/num_kv_heads).
- * max_blocks (<= block_table_stride) is the number of table columns used; the
+ * max_blocks (<= block_table_stride) is the number of table columns used
+ * (block_table_stride 0: every sequence reads row 0, e.g. the query rows of one
+ * prompt chunk over that sequence's table); the
  * reference's optional max_context_len maps to
  * max_blocks = min(ceil(max_context_len/block_size), block_table_stride).
  * context_lens[b] <= 0 reproduces the reference's all-masked softmax over the

@@ -174,6 +174,11 @@ typedef struct tv_llama_prefill_args {
   int32_t* next_token;          /* [1] greedy token after the last position, or NULL */
   void* workspace;
   size_t workspace_bytes;
+  /* 0: the reference's prefill, attending within this chunk only (llama.py:184;
+   * a chunk at start_pos > 0 ignores the cached prefix).  1: each token attends
+   * to every cached position up to its own (chunked prefill; no reference
+   * counterpart), through the paged cache after the chunk's K/V are written. */
+  int attend_prefix;
 } tv_llama_prefill_args;
 
 /* Workspace of tv_llama_prefill.  Host-only. */

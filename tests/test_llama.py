@@ -331,6 +331,35 @@ def test_prefill_matches_oracle(dtype):
     check_caches(kv, rk, rv)
 
 
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_chunked_prefill_attends_to_prefix(dtype):
+    """attend_prefix=True (no reference counterpart: the reference's chunk at
+    start_pos > 0 ignores the cached prefix, llama.py:184): a prompt prefilled
+    in chunks of 37, 50 (>= 32 rows: the scheduled decode launch) and 5 rows
+    gives each chunk the logits of one prefill of the whole prompt (oracle); the
+    default still attends within the chunk only."""
+    cfg = small_config(dtype=dtype)
+    model, kv, bm, ref, rk, rv = build(cfg, seed=8)
+    rng = np.random.default_rng(25)
+    chunks = [rng.integers(0, cfg.vocab_size, n) for n in (37, 50, 5)]
+    bm.register_sequence(0)
+    model.prefill(chunks[0], kv, bm, 0, logits=None)
+    got = [model.prefill(chunks[1], kv, bm, 0, 37, attend_prefix=True)[0].cpu().numpy(),
+           model.prefill(chunks[2], kv, bm, 0, 87, attend_prefix=True)[0].cpu().numpy()]
+    table = np.array(bm.get_block_table(0))
+    full = ref.prefill(np.concatenate(chunks), rk, rv, table, 0, 16)
+    assert max_err(got[0], full[37:87]) < LOGIT_TOL[dtype]
+    assert max_err(got[1], full[87:]) < LOGIT_TOL[dtype]
+    # the reference's behaviour (chunk only) is unchanged by default
+    model2, kv2, bm2, ref2, rk2, rv2 = build(cfg, seed=8)
+    bm2.register_sequence(0)
+    model2.prefill(chunks[0], kv2, bm2, 0, logits=None)
+    ref2.prefill(chunks[0], rk2, rv2, np.array(bm2.get_block_table(0)), 0, 16)
+    own = model2.prefill(chunks[1], kv2, bm2, 0, 37)[0].cpu().numpy()
+    want = ref2.prefill(chunks[1], rk2, rv2, np.array(bm2.get_block_table(0)), 37, 16)
+    assert max_err(own, want) < LOGIT_TOL[dtype]
+
+
 def prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg):
     """Prefill each sequence on both sides; returns the oracle's next tokens."""
     nxt = []

@@ -50,7 +50,7 @@ SIGNATURES = {
     "tv_llama_prefill_workspace_bytes": (_S, [_P, _I]),
     "tv_llama_prefill": (_I, [_P, _P, _P, _P]),
 }
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 

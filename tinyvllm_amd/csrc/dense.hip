@@ -488,4 +488,13 @@ void launch_advance(const AdvanceParams& p, hipStream_t s) {
   hipLaunchKernelGGL(advance_kernel, dim3(p.M), dim3(64), 0, s, p);
 }
 
+__global__ void __launch_bounds__(256) iota_kernel(int* out, int n, int base) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = base + i;
+}
+
+void launch_iota(int* out, int n, int base, hipStream_t s) {
+  hipLaunchKernelGGL(iota_kernel, dim3((n + 255) / 256), dim3(256), 0, s, out, n, base);
+}
+
 }  // namespace tv

@@ -96,9 +96,11 @@ StepLayout step_layout(const tv_llama_model* m, int B, int max_blocks, int block
   L.kst = c.take((size_t)B * kd * es);
   L.vst = c.take((size_t)B * kd * es);
   L.slots = c.take((size_t)B * 4);
+  // prefill: room for a prefix-attending chunk's unsplit paged-decode launch
+  // (its only workspace is the schedule of B + 1 ints)
   L.attn_ws_bytes = decode ? tv_paged_decode_workspace_bytes(B, m->n_heads, m->head_dim, max_blocks, block_size,
                                                              partition_size)
-                           : 0;
+                           : align_up((size_t)(B + 1) * 4, 256);
   L.attn_ws = c.take(L.attn_ws_bytes);
   L.total = c.off;
   return L;
@@ -257,6 +259,16 @@ int attend_unfused(const tv_llama_model* m, const tv_llama_cache* c, const Layer
                                 m->head_dim, c->block_size, c->num_blocks, kd, kd, dt, nullptr, s);
       if (rc != TV_OK) return rc;
     }
+  } else if (io.pargs->attend_prefix && io.pargs->start_pos > 0) {
+    // chunked prefill over the cached prefix: the chunk's k/v are in the cache
+    // now, so row i is a paged decode of context start_pos + i + 1 over the
+    // sequence's one table row (stride 0), whole context per work-group
+    const tv_llama_prefill_args* a = io.pargs;
+    const int width = a->bt_width * c->block_size;
+    rc = tv_paged_decode(io.attn, io.q, c->k_caches[l], c->v_caches[l], a->block_table, io.slots, M, m->n_heads,
+                         m->n_kv_heads, m->head_dim, c->block_size, c->num_blocks, 0, a->bt_width, scale, dt, dt,
+                         (width + 15) / 16 * 16, io.attn_ws, io.attn_ws_bytes, s);
+    if (rc != TV_OK) return rc;
   } else {
     rc = tv_flash_prefill(io.attn, io.q, io.kst, io.vst, M, M, m->n_heads, m->n_kv_heads, m->head_dim,
                           m->head_dim, qd, kd, kd, qd, 1, scale, dt, dt, 0, nullptr, 0, s);
@@ -562,9 +574,18 @@ int tv_llama_prefill(const tv_llama_model* m, const tv_llama_cache* c, const tv_
   io.pargs = a;
   io.kst = at<void>(ws, L.kst);
   io.vst = at<void>(ws, L.vst);
+  io.slots = at<int>(ws, L.slots);
+  io.attn_ws = at<void>(ws, L.attn_ws);
+  io.attn_ws_bytes = L.attn_ws_bytes;
   io.ks_qkv = L.ks_qkv;
   io.ks_o = L.ks_o;
   io.ks_2 = L.ks_2;
+  if (a->attend_prefix && a->start_pos > 0) {
+    // context of chunk row i: positions 0 .. start_pos + i (held in the slots region, unused by prefill)
+    tv::launch_iota(io.slots, M, a->start_pos + 1, s);
+    rc = check_launch("tv_llama_prefill");
+    if (rc != TV_OK) return rc;
+  }
   rc = run_layers(m, c, io, s);
   if (rc != TV_OK) return rc;
   unsigned long long* keys = at<unsigned long long>(ws, L.keys);

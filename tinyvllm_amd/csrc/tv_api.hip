@@ -83,7 +83,7 @@ int vec_width(std::initializer_list<long long> sizes, std::initializer_list<cons
 
 extern "C" {
 
-int tv_abi_version(void) { return 5; }
+int tv_abi_version(void) { return 6; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
@@ -146,8 +146,8 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return fail(TV_EINVAL, "tv_paged_decode: bad head counts (num_seqs=%d, num_heads=%d, num_kv_heads=%d)",
                 num_seqs, num_heads, num_kv_heads);
-  if (block_size <= 0 || num_blocks <= 0 || block_table_stride <= 0 || max_blocks <= 0 ||
-      max_blocks > block_table_stride)
+  if (block_size <= 0 || num_blocks <= 0 || block_table_stride < 0 || max_blocks <= 0 ||
+      (block_table_stride > 0 && max_blocks > block_table_stride))
     return fail(TV_EINVAL, "tv_paged_decode: bad block geometry (block_size=%d, num_blocks=%d, stride=%d, max_blocks=%d)",
                 block_size, num_blocks, block_table_stride, max_blocks);
   if ((long long)max_blocks * block_size > (1LL << 30))

@@ -100,5 +100,7 @@ void launch_norm(const NormParams& p, int dtype, hipStream_t s);
 void launch_qkv_rope(const QKVParams& p, int dtype, hipStream_t s);
 void launch_rope_table(float* table, int max_pos, int head_dim, float theta, hipStream_t s);
 void launch_advance(const AdvanceParams& p, hipStream_t s);
+// out[i] = base + i, i < n
+void launch_iota(int* out, int n, int base, hipStream_t s);
 
 }  // namespace tv

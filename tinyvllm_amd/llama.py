@@ -179,7 +179,7 @@ class _DecodeArgs(ctypes.Structure):
 class _PrefillArgs(ctypes.Structure):
     _fields_ = [("num_tokens", _I), ("tokens", _P), ("start_pos", _I), ("block_table", _P), ("bt_width", _I),
                 ("logits", _P), ("logits_last_only", _I), ("next_token", _P), ("workspace", _P),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("attend_prefix", _I)]
 
 
 def _ptr_array(tensors):
@@ -274,19 +274,24 @@ class Llama:
         return s, keep
 
     # ---- prefill ---------------------------------------------------------------
-    def prefill(self, tokens, kv_cache, block_manager, seq_id, start_pos=0, *, logits="all"):
+    def prefill(self, tokens, kv_cache, block_manager, seq_id, start_pos=0, *, logits="all", attend_prefix=False):
         """Prompt pass of one sequence (llama.py:264-285).  Returns logits
-        [1, L, vocab] float32 (``logits="last"``: [1, 1, vocab]; ``None``: no logits)."""
+        [1, L, vocab] float32 (``logits="last"``: [1, 1, vocab]; ``None``: no logits).
+        ``attend_prefix`` (keyword-only, not in the reference): a chunk at
+        ``start_pos > 0`` attends to the cached prefix as well; the reference's
+        prefill attends within the chunk only (llama.py:184)."""
         toks = _i32(tokens, self.device).reshape(-1)
         n = toks.numel()
         for pos in range(start_pos, start_pos + n):            # llama.py:206, at layer 0
             block_manager.ensure_block_for_position(seq_id, pos)
-        out = self.prefill_table(toks, kv_cache, block_manager.get_block_table(seq_id), start_pos, logits=logits)
+        out = self.prefill_table(toks, kv_cache, block_manager.get_block_table(seq_id), start_pos, logits=logits,
+                                 attend_prefix=attend_prefix)
         for _ in range(n):                                     # llama.py:282-283
             block_manager.advance_position(seq_id)
         return out
 
-    def prefill_table(self, tokens, kv_cache, block_table, start_pos=0, *, logits="all", next_token=None):
+    def prefill_table(self, tokens, kv_cache, block_table, start_pos=0, *, logits="all", next_token=None,
+                      attend_prefix=False):
         """Prompt pass over an explicit block table (the table must cover every
         position).  ``next_token``: an int32 device tensor slice that receives the
         greedy token after the last position."""
@@ -310,7 +315,7 @@ class Llama:
         args = _PrefillArgs(n, toks.data_ptr(), start_pos, table.data_ptr(), table.numel(),
                             out.data_ptr() if out is not None else None, 1 if logits == "last" else 0,
                             next_token.data_ptr() if next_token is not None else None,
-                            self._prefill_ws.data_ptr(), self._prefill_ws.numel())
+                            self._prefill_ws.data_ptr(), self._prefill_ws.numel(), 1 if attend_prefix else 0)
         _lib.check(lib.tv_llama_prefill(ctypes.byref(self._model), ctypes.byref(cache), ctypes.byref(args),
                                         _lib.stream_ptr(self.device)), "tv_llama_prefill")
         del keep
