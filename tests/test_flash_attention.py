@@ -250,6 +250,27 @@ def test_varlen_matches_per_prompt(lens, hq, hkv, d, causal, dtype):
         s += n
 
 
+def test_varlen_fp32_output_and_strided_inputs():
+    """fp32 output, and q/k/v as views into one fused [T, (Hq + 2 Hkv) * D] buffer."""
+    from tinyvllm_amd.attention import flash_prefill_varlen
+    lens = [70, 3, 130]
+    tot, hq, hkv, d = sum(lens), 8, 2, 64
+    fused = randn(70, tot, (hq + 2 * hkv) * d, dtype=torch.bfloat16).cuda()
+    q = fused[:, :hq * d].view(tot, hq, d)
+    k = fused[:, hq * d:(hq + hkv) * d].view(tot, hkv, d)
+    v = fused[:, (hq + hkv) * d:].view(tot, hkv, d)
+    out = flash_prefill_varlen(q, k, v, lens, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    s = 0
+    for n in lens:
+        sl = slice(s, s + n)
+        want = flash_prefill_ref(q[sl].float().cpu().numpy()[None], k[sl].float().cpu().numpy()[None],
+                                 v[sl].float().cpu().numpy()[None], True)[0]
+        assert np.abs(out[sl].cpu().numpy() - want).max() <= TOL[torch.bfloat16], n
+        s += n
+
+
 def test_varlen_plan_replays_in_graph():
     """The plan captured in a HIP graph: replays (with eager work between them)
     equal the eager launch."""

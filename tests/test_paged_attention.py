@@ -304,3 +304,24 @@ def test_random_shapes(i, hq, hkv, d, bs, width, ctx, dtype, psize):
                                   dtype, width=width)
     kw = {} if psize is None else {"partition_size": psize}
     check((q, kc, vc, bt, ctx), hq, hkv, d, bs, dtype, **kw)
+
+
+def test_shared_table_row_stride_zero():
+    """block_table_stride 0: every query row reads table row 0 (the query rows of
+    one prompt chunk over its sequence's table); equals the same table repeated."""
+    from tinyvllm_amd import _lib
+    ctx = [5, 16, 17, 40, 64]
+    q, kc, vc, bt, _ = build_case(42, [64] * len(ctx), 8, 2, 64, 16, torch.float16)
+    row = bt[:1].copy()
+    cl = np.asarray(ctx, np.int32)
+    dev = "cuda"
+    out = torch.empty((len(ctx), 1, 8, 64), dtype=torch.float16, device=dev)
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    row_d, cl_d = torch.from_numpy(row).to(dev), torch.from_numpy(cl).to(dev)
+    rc = _lib.load().tv_paged_decode(out.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), row_d.data_ptr(),
+                                     cl_d.data_ptr(), len(ctx), 8, 2, 64, 16, kc.shape[0], 0, row.shape[1],
+                                     0.125, _lib.TV_F16, _lib.TV_F16, 64 * 16, None, 0, None)
+    _lib.check(rc, "tv_paged_decode")
+    torch.cuda.synchronize()
+    want = oracle(q, kc, vc, np.repeat(row, len(ctx), 0), cl, 8, 2, 64, 16)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[torch.float16]
