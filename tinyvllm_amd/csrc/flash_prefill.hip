@@ -718,7 +718,14 @@ int launch_flash_prefill_varlen(const PrefillParams& p_in, int num_seqs, int max
   const long long wgs = (long long)pp.num_heads * ((total_q + kPrefillBM - 1) / kPrefillBM + num_seqs);
   const bool d64 = pp.head_dim == 64;
   const bool long_rows = prefill_key_tiles_host(pp, nqt - 1) >= 8;
-  const int cfg = long_rows && wgs <= 256 ? 0 : (d64 && long_rows && wgs < 1024 ? 2 : 1);
+  // One prompt: the single-prompt choice.  Several: one key group of 4 waves
+  // unless everything fits one work-group per CU -- the shorter prompts' work
+  // groups fill the slots the long rows leave, so more resident work-groups
+  // beat halving the longest chain (MI355X, fp16 D 64: L 512 + 1024 in 15.2
+  // against 17.8 us with two key groups of 32-key tiles; 16 x 64 tokens 5.6
+  // against 6.7; 1024 + 1024 + 512 + 256 22.7 against 26.9).
+  const int cfg = long_rows && wgs <= 256 ? 0
+                  : (num_seqs == 1 && d64 && long_rows && wgs < 1024 ? 2 : 1);
   if (dtype == kF16) {
     if (d64) launch_fa<_Float16, 64>(cfg, grid, pp, stream);
     else launch_fa<_Float16, 128>(cfg, grid, pp, stream);
