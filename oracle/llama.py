@@ -15,6 +15,8 @@ Follows tinyvllm/model/llama.py step by step:
 * ``LlamaRef.forward``  the dense causal forward over a whole token list (no cache): what
                         prefill + decode must reproduce position by position
 * greedy sampling       sample_tokens with temperature 0 -> argmax, sampling.py:131-134
+* ``round_bf16``        storage rounding of a bfloat16 cache (no reference counterpart:
+                        the reference has no bfloat16, weights.py:44)
 
 Arithmetic is float32 (the north-star reference precision); the paged cache stores
 ``cache_dtype`` (float16 by default, as KVCache(dtype=float16), kv_cache.py:25-32).
@@ -52,6 +54,15 @@ def apply_rope_ref(x, cos, sin):
     return np.stack([out0, out1], axis=-1).reshape(x.shape).astype(np.float32)
 
 
+def round_bf16(x):
+    """Round float32 values to the nearest bfloat16 (ties to even), returned as
+    float32: the storage rounding of a bfloat16 cache or activation.  NaN is
+    not expected here (finite model values only)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return r.astype(np.uint32).view(np.float32)
+
+
 def silu_ref(x):
     return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
 
@@ -65,6 +76,8 @@ class LlamaRef:
     """The reference model's forward passes over numpy float32 weights."""
 
     def __init__(self, cfg, weights, cache_dtype=np.float16):
+        """``cache_dtype``: a numpy dtype the cache rows are rounded through, or
+        ``"bfloat16"`` (rounded with ``round_bf16``)."""
         self.cfg = cfg
         self.w = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
         self.cache_dtype = cache_dtype
@@ -99,7 +112,11 @@ class LlamaRef:
         return self._lin(rms_norm_ref(x, self.w["norm.weight"], self.cfg.norm_eps), "output.weight")
 
     def _store(self, cache, slot, value, block_size):
-        cache.reshape(-1, *cache.shape[2:])[slot] = value.astype(self.cache_dtype).astype(cache.dtype)
+        if isinstance(self.cache_dtype, str) and self.cache_dtype == "bfloat16":
+            rounded = round_bf16(value)
+        else:
+            rounded = value.astype(self.cache_dtype)
+        cache.reshape(-1, *cache.shape[2:])[slot] = rounded.astype(cache.dtype)
 
     def forward(self, tokens):
         """Dense causal forward over tokens [L] from position 0: logits [L, vocab]."""
@@ -127,12 +144,22 @@ class LlamaRef:
         return self._logits(x)
 
     def decode(self, tokens, positions, context_lens, block_tables, k_caches, v_caches, block_size,
-               write_before_attend=True):
-        """One batched decode step (llama.py:290-388); writes the caches; logits [B, vocab]."""
+               write_before_attend=True, max_blocks=None):
+        """One batched decode step (llama.py:290-388); writes the caches; logits [B, vocab].
+
+        ``block_tables`` lists every block of each sequence: the K/V of position p
+        go to column p // block_size (the block get_slot returns, llama.py:382).
+        Attention reads the first ``max_blocks`` columns (all when None), padded
+        with block 0 when the table is narrower (llama.py:368-374)."""
         c, d = self.cfg, self.head_dim
         tokens = np.asarray(tokens).reshape(-1)
         positions = np.asarray(positions).reshape(-1)
         block_tables = np.asarray(block_tables)
+        attend_tables = block_tables
+        if max_blocks is not None:
+            attend_tables = np.zeros((block_tables.shape[0], max_blocks), block_tables.dtype)
+            n = min(max_blocks, block_tables.shape[1])
+            attend_tables[:, :n] = block_tables[:, :n]
         x = self.w["tok_embeddings.weight"][tokens]
         slots = block_tables[np.arange(len(tokens)), positions // block_size] * block_size + positions % block_size
         for i in range(c.n_layers):
@@ -140,7 +167,7 @@ class LlamaRef:
             if write_before_attend:
                 self._store(k_caches[i], slots, k, block_size)
                 self._store(v_caches[i], slots, v, block_size)
-            attn = paged_decode_ref(q[:, None], k_caches[i], v_caches[i], block_tables, context_lens,
+            attn = paged_decode_ref(q[:, None], k_caches[i], v_caches[i], attend_tables, context_lens,
                                     c.n_heads, c.n_kv_heads, d, block_size, acc=np.float32)[:, 0]
             if not write_before_attend:
                 self._store(k_caches[i], slots, k, block_size)

@@ -1,0 +1,162 @@
+"""End-to-end greedy decode of random-init TinyLlama-1.1B at the benchmark's own workload.
+
+The workload is exactly what bench.py times (tinyvllm_amd.workloads.e2e_tinyllama_b64):
+22 layers, dim 2048, 32 / 4 heads, MLP 5632, vocab 32000, fp16 weights ~ N(0, 0.02),
+64 prompts of 1024 seeded tokens prefilled into a paged cache (block_size 16, a
+shuffled pool of the need + 10%, 72-block tables), then greedy decode steps
+replayed from one captured HIP graph (Llama.prefill, Llama.create_jit_decode,
+Llama.decode: tinyvllm/model/llama.py:264-388; greedy: sampling.py:131-134).
+
+Checks against the float32 oracle (oracle/llama.py), fed with the K/V rows the
+device wrote (gathered into a compact cache for the checked sequences):
+
+* one 1024-token prompt through the oracle's prefill: last-position logits
+  within 2e-2 and sampled cache rows of every layer;
+* step-1 logits of 4 sequences (first, last and two seeded picks) within 2e-2;
+* 128 device-side steps: the first 8 equal 8 host-driven steps bit for bit,
+  and 2 sequences teacher-forced through the oracle for 8 steps keep their
+  logits within 2e-2; the greedy token must match wherever the oracle's top two
+  logits are more than 2 x 2e-2 apart (near ties may flip either way), and the
+  raw match rate is printed.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.llama import LlamaRef, greedy_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def e2e():
+    from tinyvllm_amd import workloads
+    from tinyvllm_amd.llama import random_weights
+    wl = workloads.e2e_tinyllama_b64()
+    m, kv = wl.model, wl.kv
+    B, L = wl.batch, wl.prompt_len
+    first = torch.zeros(B, dtype=torch.int32, device="cuda")
+    for b in range(B):
+        m.prefill_table(wl.prompts[b], kv, wl.tables[b], 0, logits=None, next_token=first[b:b + 1])
+    torch.cuda.synchronize()
+    _say(f"e2e: prefilled {B} x {L} tokens")
+    # the oracle's weights: the same seeded draw, unfused, float32 on the host
+    w = {}
+    for name, t in random_weights(m.config, seed=wl.seed).items():
+        w[name] = t.float().cpu().numpy()
+        del t
+    torch.cuda.empty_cache()
+    ref = LlamaRef(m.config, w, cache_dtype=np.float16)
+    _say("e2e: oracle weights ready")
+    yield wl, first, ref
+    del wl
+    torch.cuda.empty_cache()
+
+
+def compact_cache(wl, seqs, ncols):
+    """The first ``ncols`` table blocks of ``seqs`` gathered from the device into
+    per-layer float32 caches, and the remapped [len(seqs), ncols] tables."""
+    ids = np.concatenate([wl.tables[b, :ncols] for b in seqs]).astype(np.int64)
+    sel = torch.from_numpy(ids).cuda()
+    kc = [k.index_select(0, sel).float().cpu().numpy() for k in wl.kv.k_cache]
+    vc = [v.index_select(0, sel).float().cpu().numpy() for v in wl.kv.v_cache]
+    tables = np.arange(len(ids), dtype=np.int32).reshape(len(seqs), ncols)
+    return kc, vc, tables
+
+
+def test_prefill_1024_matches_oracle(e2e):
+    wl, first, ref = e2e
+    m, kv = wl.model, wl.kv
+    b = 5
+    got = m.prefill_table(wl.prompts[b], kv, wl.tables[b], 0, logits="last")[0, 0].cpu().numpy()
+    nb = wl.prompt_len // 16
+    shape = (nb, 16, m.config.n_kv_heads, m.config.head_dim)
+    rk = [np.zeros(shape, np.float32) for _ in range(m.config.n_layers)]
+    rv = [np.zeros(shape, np.float32) for _ in range(m.config.n_layers)]
+    want = ref.prefill(wl.prompts[b], rk, rv, np.arange(nb, dtype=np.int32), 0, 16)[-1]
+    err = float(np.abs(got - want).max())
+    _say(f"e2e prefill L1024 seq {b}: last-logit max-abs {err:.3e} (logit scale {np.abs(want).max():.3f})")
+    assert err <= TOL
+    assert int(first[b]) == int(np.argmax(got))
+    kc, vc, _ = compact_cache(wl, [b], nb)
+    rows = np.random.Generator(np.random.PCG64(3)).choice(wl.prompt_len, 48, replace=False)
+    for layer in range(m.config.n_layers):
+        for dev, host in ((kc[layer], rk[layer]), (vc[layer], rv[layer])):
+            d = dev.reshape(nb * 16, -1)[rows]
+            h = host.reshape(nb * 16, -1)[rows]
+            bound = 4e-3 * max(1.0, float(np.abs(host).max()))
+            assert float(np.abs(d - h).max()) <= bound, layer
+
+
+def test_step1_logits_match_oracle(e2e):
+    from tinyvllm_amd.llama import DecodeGraph
+    wl, first, ref = e2e
+    m, kv = wl.model, wl.kv
+    B, L = wl.batch, wl.prompt_len
+    g = DecodeGraph(m, kv, B, wl.tables.shape[1])
+    g.set_inputs(first, [L] * B, [L + 1] * B, wl.tables)
+    g.step()
+    logits = g.logits.cpu().numpy()
+    g.close()
+    seqs = sorted({0, B - 1, *np.random.Generator(np.random.PCG64(4)).choice(B, 2, replace=False).tolist()})
+    ncols = L // 16 + 1
+    kc, vc, tables = compact_cache(wl, seqs, ncols)
+    n = len(seqs)
+    want = ref.decode(first.cpu().numpy()[seqs], [L] * n, [L + 1] * n, tables, kc, vc, 16)
+    err = float(np.abs(logits[seqs] - want).max())
+    match = float(np.mean(np.argmax(logits[seqs], 1) == greedy_ref(want)))
+    _say(f"e2e step 1, sequences {seqs}: logits max-abs {err:.3e}, greedy match {match:.2f}")
+    assert err <= TOL
+    assert np.array_equal(np.argmax(logits, 1), g.tokens.cpu().numpy())
+
+
+def test_128_device_steps_equal_host_steps_and_oracle(e2e):
+    from tinyvllm_amd.llama import DecodeGraph
+    wl, first, ref = e2e
+    m, kv = wl.model, wl.kv
+    B, L, steps, check = wl.batch, wl.prompt_len, wl.decode_steps, 8
+    g = DecodeGraph(m, kv, B, wl.tables.shape[1], keep_logits=False, history_len=L + steps + 2)
+    g.set_inputs(first, [L] * B, [L + 1] * B, wl.tables)
+    g.run(steps)
+    torch.cuda.synchronize()
+    hist = g.history.cpu().numpy()
+    assert g.positions.cpu().tolist() == [L + steps] * B
+    assert (hist[:, L + 1:L + 1 + steps] >= 0).all() and (hist[:, L + 1:L + 1 + steps] < 32000).all()
+    g.close()
+    _say(f"e2e: {steps} device steps done")
+    # host-driven steps (tokens copied in every step) reproduce the device loop
+    h = DecodeGraph(m, kv, B, wl.tables.shape[1])
+    cur = first.clone()
+    inputs, step_logits = [], []
+    for i in range(check):
+        inputs.append(cur.cpu().numpy())
+        h.set_inputs(cur, [L + i] * B, [L + i + 1] * B, wl.tables)
+        h.step()
+        cur = h.tokens.clone()
+        step_logits.append(h.logits.cpu().numpy())
+        assert np.array_equal(cur.cpu().numpy(), hist[:, L + 1 + i]), i
+    h.close()
+    # teacher-forced oracle over the device's own tokens and K/V rows
+    seqs = [3, 40]
+    kc, vc, tables = compact_cache(wl, seqs, (L + check) // 16 + 1)
+    matches, clear_ok = [], True
+    for i in range(check):
+        toks = [int(inputs[i][b]) for b in seqs]
+        want = ref.decode(toks, [L + i] * 2, [L + i + 1] * 2, tables, kc, vc, 16)
+        got = step_logits[i][seqs]
+        err = float(np.abs(got - want).max())
+        assert err <= TOL, f"step {i}: max-abs {err}"
+        top2 = np.sort(want, axis=1)[:, -2:]
+        clear = top2[:, 1] - top2[:, 0] > 2 * TOL
+        gt = np.argmax(got, 1)
+        clear_ok &= bool(np.array_equal(gt[clear], greedy_ref(want)[clear]))
+        matches += (gt == greedy_ref(want)).tolist()
+    _say(f"e2e teacher-forced sequences {seqs} x {check} steps: greedy match rate {np.mean(matches):.3f}")
+    assert clear_ok

@@ -289,7 +289,8 @@ def build(cfg, seed=0, std=0.05, write_before_attend=True, num_blocks=64, block_
     model = Llama(cfg, weights, write_before_attend=write_before_attend)
     kv = KVCache(cfg.n_layers, num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
     bm = BlockManager(1, num_blocks, block_size)
-    ref = LlamaRef(cfg, numpy_weights(weights), cache_dtype=np.float32 if cfg.dtype == torch.float32 else np.float16)
+    cache_dtype = {torch.float32: np.float32, torch.float16: np.float16, torch.bfloat16: "bfloat16"}[cfg.dtype]
+    ref = LlamaRef(cfg, numpy_weights(weights), cache_dtype=cache_dtype)
     shape = (num_blocks, block_size, cfg.n_kv_heads, cfg.head_dim)
     rk = [np.zeros(shape, np.float32) for _ in range(cfg.n_layers)]
     rv = [np.zeros(shape, np.float32) for _ in range(cfg.n_layers)]
@@ -301,19 +302,19 @@ def max_err(got, want):
 
 
 def check_caches(kv, rk, rv):
-    """Caches vs the oracle's: a few fp16 ulps of the largest entry for fp16
-    (layer-0 rounding differences propagate into the later layers' k/v), the
-    fp32 bar of 1e-4 relative for fp32 (summation order differs from numpy's)."""
-    rel = 1e-4 if kv.dtype == torch.float32 else 4e-3
+    """Caches vs the oracle's: a few 16-bit ulps of the largest entry for fp16 /
+    bf16 (layer-0 rounding differences propagate into the later layers' k/v),
+    the fp32 bar of 1e-4 relative for fp32 (summation order differs from numpy's)."""
+    rel = {torch.float32: 1e-4, torch.float16: 4e-3, torch.bfloat16: 2e-2}[kv.dtype]
     for layer, (k, v) in enumerate(zip(rk, rv)):
         for got, want in ((kv.k_cache[layer], k), (kv.v_cache[layer], v)):
             bound = rel * max(1.0, float(np.abs(want).max()))
             assert max_err(got.float().cpu().numpy(), want) < bound, layer
 
 
-# fp16 logits within 2e-2 of the float32 oracle (the fp16 bar); fp32 models (the
-# reference's default dtype, weights.py:32) within 1e-4
-LOGIT_TOL = {"float16": TOL, "float32": 1e-4}
+# fp16 / bf16 logits within 2e-2 of the float32 oracle (the 16-bit bar); fp32
+# models (the reference's default dtype, weights.py:32) within 1e-4
+LOGIT_TOL = {"float16": TOL, "bfloat16": TOL, "float32": 1e-4}
 
 
 @pytest.mark.parametrize("dtype", ["float16", "float32"])
@@ -514,3 +515,143 @@ def test_tinyllama_shape_matches_oracle():
         got_tok = logits[:, 0].cpu().numpy().argmax(1)
         assert np.array_equal(got_tok[clear], greedy_ref(want)[clear])
         nxt = [int(t) for t in greedy_ref(want)]
+
+
+def engine_tables(bm, seq_ids, width):
+    """LLMEngine._prepare_batch_tensors (engine.py:235-255): each sequence's
+    current table, zero padded -- built before get_slot allocates."""
+    bt = np.zeros((len(seq_ids), width), np.int32)
+    for i, s in enumerate(seq_ids):
+        t = bm.get_block_table(s)[:width]
+        bt[i, :len(t)] = t
+    return bt
+
+
+@pytest.mark.parametrize("write_before_attend", [True, False])
+def test_decode_allocates_the_new_block_like_get_slot(write_before_attend):
+    """Driven the engine's way: tables from get_block_table with no allocation,
+    context = position + 1 (engine.py:152-153, 235-255).  Prompts of 16 and 32
+    tokens start their first decode position in a block the table does not list
+    yet; Llama.decode must allocate it through get_slot (llama.py:381-386) and
+    write the token's K/V there.  Block 0 -- the last one LIFO allocation hands
+    out, so no sequence owns it here -- stays untouched, the logits and caches
+    match the oracle given the table after the allocation, and the tables grow
+    by one block per 16 positions.  (In the reference order the attended row of
+    the new position is unwritten -- zero in a fresh cache -- as in the
+    reference, quirk Q4.)"""
+    cfg = small_config()
+    model, kv, bm, ref, rk, rv = build(cfg, seed=9, num_blocks=24, write_before_attend=write_before_attend)
+    rng = np.random.default_rng(26)
+    lens = [16, 5, 32]
+    toks = prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg)
+    jit = model.create_jit_decode(16)
+    max_blocks = 8
+    seqs = [0, 1, 2]
+    for step in range(18):
+        pos = [bm.get_context_length(s) for s in seqs]
+        before = [len(bm.get_block_table(s)) for s in seqs]
+        bt = engine_tables(bm, seqs, max_blocks)
+        ctx = [p + 1 for p in pos]
+        logits = model.decode(torch.tensor(toks).reshape(-1, 1), kv, bm, seqs, pos, torch.from_numpy(bt),
+                              torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
+        after = [len(bm.get_block_table(s)) for s in seqs]
+        assert after == [b + (p % 16 == 0 and p // 16 == b) for b, p in zip(before, pos)], step
+        full = engine_tables(bm, seqs, max_blocks)
+        want = ref.decode(toks, pos, ctx, full, rk, rv, 16, write_before_attend=write_before_attend)
+        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        assert [bm.get_context_length(s) for s in seqs] == [p + 1 for p in pos]
+        toks = [int(t) for t in greedy_ref(want)]
+    assert all(0 not in bm.get_block_table(s) for s in seqs)
+    for k, v in zip(kv.k_cache, kv.v_cache):
+        assert not k[0].any() and not v[0].any()
+    check_caches(kv, rk, rv)
+
+
+def test_decode_past_the_table_width_writes_kv_and_truncates_attention():
+    """Quirk Q5 (engine.py:81, llama.py:368-374): a position past max_blocks
+    columns is still written to its block (get_slot, llama.py:382) while
+    attention covers only the first max_blocks * block_size tokens."""
+    cfg = small_config()
+    model, kv, bm, ref, rk, rv = build(cfg, seed=10, num_blocks=16)
+    rng = np.random.default_rng(27)
+    lens = [40, 20]
+    toks = prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg)
+    jit = model.create_jit_decode(16)
+    max_blocks = 2
+    for step in range(2):
+        pos = [bm.get_context_length(s) for s in (0, 1)]
+        bt = engine_tables(bm, [0, 1], 3)
+        ctx = [p + 1 for p in pos]
+        logits = model.decode(torch.tensor(toks).reshape(-1, 1), kv, bm, [0, 1], pos, torch.from_numpy(bt),
+                              torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
+        full = engine_tables(bm, [0, 1], 3)
+        want = ref.decode(toks, pos, ctx, full, rk, rv, 16, max_blocks=max_blocks)
+        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        toks = [int(t) for t in greedy_ref(want)]
+    check_caches(kv, rk, rv)
+    slot = bm.get_block_table(0)[41 // 16] * 16 + 41 % 16
+    assert kv.k_cache[1].reshape(-1, cfg.n_kv_heads * cfg.head_dim)[slot].abs().sum() > 0
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("block_size", [4, 32])
+@pytest.mark.parametrize("ctx_convention", ["cached", "engine"])
+def test_decode_block_sizes_match_oracle(ctx_convention, block_size, dtype):
+    """Restates test_multiple_blocks_context (tests/test_jit_decode.py:259-294:
+    block_size 4, contexts spanning several blocks) for 16-bit models at block
+    sizes 4 (not a multiple of 16: the unfused RoPE + K/V write and the VALU
+    paged decode) and 32 (the fused step attention), with the reference test's
+    context (= tokens cached, ctx = position) and the engine's (position + 1)."""
+    cfg = small_config(dim=256, n_heads=4, n_kv_heads=2, max_seq_len=256, dtype=dtype)
+    model, kv, bm, ref, rk, rv = build(cfg, seed=12, num_blocks=128, block_size=block_size)
+    rng = np.random.default_rng(28)
+    lens = [10, 33, 90]
+    toks = prefill_batch(model, kv, bm, ref, rk, rv, lens, rng, cfg)
+    jit = model.create_jit_decode(block_size)
+    max_blocks = -(-(max(lens) + 8) // block_size)
+    seqs = [0, 1, 2]
+    for step in range(4):
+        pos = [bm.get_context_length(s) for s in seqs]
+        for s, p in zip(seqs, pos):                       # _setup_seq pre-allocates (test_jit_decode.py:268)
+            bm.ensure_block_for_position(s, p)
+        bt = engine_tables(bm, seqs, max_blocks)
+        ctx = pos if ctx_convention == "cached" else [p + 1 for p in pos]
+        logits = model.decode(torch.tensor(toks).reshape(-1, 1), kv, bm, seqs, pos, torch.from_numpy(bt),
+                              torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
+        assert logits.shape == (3, 1, cfg.vocab_size) and not logits.isnan().any()
+        want = ref.decode(toks, pos, ctx, bt, rk, rv, block_size)
+        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        toks = [int(t) for t in greedy_ref(want)]
+    check_caches(kv, rk, rv)
+
+
+def test_load_weights_sets_found_names_and_keeps_the_rest():
+    """Llama.load_weights follows llama.py:390-401: names are mapped (Meta, HF and
+    the fallback rewrites), names the model lacks are ignored, and weights the
+    dict does not hold keep their values.  The fused layouts (wq|wk|wv, the
+    interleaved w1/w3) receive the parts in place; a wrong shape raises."""
+    from tinyvllm_amd.llama import Llama, random_weights
+    cfg = small_config()
+    src = random_weights(cfg, seed=3)
+    part = {"layers.0.feed_forward.w1.weight": src["layers.0.feed_forward.w1.weight"],
+            "model.layers.1.self_attn.k_proj.weight": src["layers.1.attention.wk.weight"],
+            "model.layers.1.mlp.up_proj.weight": src["layers.1.feed_forward.w3.weight"],
+            "lm_head.weight": src["output.weight"],
+            "model.layers.0.post_attention_layernorm.weight": src["layers.0.ffn_norm.weight"] * 2,
+            "model.rotary_emb.inv_freq": torch.zeros(7)}
+    expected = random_weights(cfg, seed=11)
+    expected.update({"layers.0.feed_forward.w1.weight": src["layers.0.feed_forward.w1.weight"],
+                     "layers.1.attention.wk.weight": src["layers.1.attention.wk.weight"],
+                     "layers.1.feed_forward.w3.weight": src["layers.1.feed_forward.w3.weight"],
+                     "output.weight": src["output.weight"],
+                     "layers.0.ffn_norm.weight": src["layers.0.ffn_norm.weight"] * 2})
+    want = Llama(cfg, expected)
+    for model in (Llama(cfg, seed=11), Llama(cfg, part, seed=11)):
+        model.load_weights(part)
+        for a, b in zip([model.tok_embeddings, model.output, model.norm, *model.wqkv, *model.wo, *model.w13,
+                         *model.w2, *model.attention_norm, *model.ffn_norm],
+                        [want.tok_embeddings, want.output, want.norm, *want.wqkv, *want.wo, *want.w13,
+                         *want.w2, *want.attention_norm, *want.ffn_norm]):
+            assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        want.load_weights({"output.weight": torch.zeros(3, 3)})

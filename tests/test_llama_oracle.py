@@ -243,3 +243,47 @@ def test_prefill_slots_follow_block_manager():
     written = np.nonzero(np.abs(kc[0]).reshape(12 * 4, -1).sum(-1))[0]
     table = bm.get_block_table(0)
     assert sorted(written.tolist()) == sorted(table[p // 4] * 4 + p % 4 for p in range(10))
+
+
+def test_round_bf16_matches_torch():
+    """round_bf16 equals torch's float32 -> bfloat16 conversion (round to nearest,
+    ties to even) bit for bit, including ties, subnormals and large values; a
+    truncating conversion (the plausible mistake) differs."""
+    from oracle.llama import round_bf16
+    rng = np.random.default_rng(12)
+    x = np.concatenate([rng.standard_normal(4096).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 4096),
+                        np.array([0.0, -0.0, 1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 3e38, 1e-40, -1e-40],
+                                 np.float32)]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = round_bf16(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    truncated = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    assert not np.array_equal(truncated, want)
+
+
+def test_decode_attention_width_truncates_context():
+    """max_blocks = m attends to the first m*bs positions (llama.py:368-374 pad /
+    truncate; the padded gather of llama.py:120-140): the same logits as a full
+    table with the context clipped to m*bs.  The K/V write still goes to the
+    block of the token's position."""
+    cfg = Cfg(n_layers=1)
+    ref = LlamaRef(cfg, rand_weights(cfg, seed=13), cache_dtype=np.float32)
+    bs, nb = 4, 16
+    table = np.random.default_rng(14).permutation(nb)[:5][None]
+    prompt = np.arange(17) % cfg.vocab_size
+    runs = []
+    for _ in range(2):
+        kc, vc = _cache(cfg, nb, bs)
+        ref.prefill(prompt, kc, vc, table[0], 0, bs)
+        runs.append((kc, vc))
+    pos = 17
+    a = ref.decode([5], [pos], [pos + 1], table, *runs[0], bs, max_blocks=3)
+    b = ref.decode([5], [pos], [3 * bs], table, *runs[1], bs)
+    assert np.abs(a - b).max() < 1e-5          # the gathers differ in width: float32 sum order only
+    slot = table[0, pos // bs] * bs + pos % bs
+    assert np.abs(runs[0][0][0].reshape(nb * bs, -1)[slot]).sum() > 0
+    # a wider attention window changes the result (the truncation is real)
+    kc, vc = _cache(cfg, nb, bs)
+    ref.prefill(prompt, kc, vc, table[0], 0, bs)
+    c = ref.decode([5], [pos], [pos + 1], table, kc, vc, bs, max_blocks=5)
+    assert np.abs(a - c).max() > 1e-4

@@ -156,8 +156,9 @@ class VarlenPrefillPlan:
     def __init__(self, queries, keys, values, seq_lens, causal=True, *, out_dtype=None):
         self.lib = _lib.load()
         self.dev = _on_gpu(queries, keys, values)
+        for t in (queries, keys, values):
+            _require(t.dim() == 3 or (t.dim() == 4 and t.shape[0] == 1), "inputs must be [T, H, D] or [1, T, H, D]")
         q, k, v = (t[0] if t.dim() == 4 else t for t in (queries, keys, values))
-        _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "inputs must be [T, H, D] or [1, T, H, D]")
         for t, name in ((q, "queries"), (k, "keys"), (v, "values")):
             _require(t.stride(2) == 1 and t.stride(1) == t.shape[2], f"{name}: heads and head_dim must be contiguous")
         tot, hq, d = q.shape
@@ -175,6 +176,7 @@ class VarlenPrefillPlan:
         self.order = torch.from_numpy(order).to(self.dev)
         out_dtype = q.dtype if out_dtype is None else out_dtype
         self.out = torch.empty((tot, hq, d), dtype=out_dtype, device=self.dev)
+        self._inputs = (queries, keys, values)     # a captured launch reads them on every replay
         self._args = (self.out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), self.cu.data_ptr(),
                       self.cu.data_ptr(), self.order.data_ptr(), len(lens), max(lens), max(lens), tot, hq, hkv, d,
                       q.stride(0), k.stride(0), v.stride(0), hq * d, 1 if causal else 0, 1.0 / math.sqrt(d),

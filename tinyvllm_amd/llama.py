@@ -211,27 +211,70 @@ class Llama:
         _lib.check(lib.tv_rope_table(self.rope.data_ptr(), self.rope_len, config.head_dim,
                                      float(config.rope_theta), _lib.stream_ptr(self.device)),
                    "tv_rope_table")
-        self.load_weights(random_weights(config, seed, device=self.device) if weights is None else weights)
+        known = self._known(weights) if weights is not None else {}
+        if len(known) == len(weight_shapes(config)):
+            self._build(known)
+        else:
+            # the reference's Llama(config) starts from random-init layers and
+            # load_weights replaces only the names it finds (llama.py:390-401)
+            self._build(random_weights(config, seed, device=self.device))
+            if known:
+                self.load_weights(known)
         self._prefill_ws = None
 
     # ---- weights -----------------------------------------------------------
+    def _known(self, weights):
+        """Canonical name -> tensor for the names of this model; others are dropped
+        (llama.py:395-398: names outside the weight map are ignored)."""
+        shapes = weight_shapes(self.config)
+        out = {}
+        for k, v in weights.items():
+            n = canonical_name(k)
+            if n in shapes:
+                t = v if isinstance(v, torch.Tensor) else torch.as_tensor(np.asarray(v))
+                if tuple(t.shape) != shapes[n]:
+                    raise ValueError(f"{k}: shape {tuple(t.shape)} != {shapes[n]}")
+                out[n] = t
+        return out
+
     def load_weights(self, weights):
-        """Load a name -> tensor dict (Meta or HF names), cast to the model dtype,
-        and build the fused layouts the kernels read: wq|wk|wv rows stacked, and
-        w1 / w3 interleaved two rows at a time (rows 4j, 4j+1 = w1 rows 2j, 2j+1;
-        rows 4j+2, 4j+3 = w3 rows 2j, 2j+1)."""
+        """Load a name -> tensor dict (Meta or HF names, llama.py:390-445), cast to
+        the model dtype.  As in the reference, names this model does not have are
+        ignored and weights missing from the dict keep their current values; a
+        tensor of the wrong shape raises ValueError.  Weights are copied into the
+        existing device storage (fused layouts included), so captured decode
+        graphs stay valid."""
         c = self.config
-        w = {canonical_name(k): v for k, v in weights.items()}
-        shapes = weight_shapes(c)
-        missing = [n for n in shapes if n not in w]
-        if missing:
-            raise KeyError(f"missing weights: {missing[:4]}{' ...' if len(missing) > 4 else ''}")
+        qd, kd, h = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim, c.hidden_dim
+        for name, t in self._known(weights).items():
+            if name == "tok_embeddings.weight":
+                dst = self.tok_embeddings
+            elif name == "output.weight":
+                dst = self.output
+            elif name == "norm.weight":
+                dst = self.norm
+            else:
+                layer, rest = name[len("layers."):].split(".", 1)
+                i = int(layer)
+                fused13 = self.w13[i].view(h // 2, 2, 2, c.dim)
+                dst = {"attention.wq.weight": self.wqkv[i][:qd], "attention.wk.weight": self.wqkv[i][qd:qd + kd],
+                       "attention.wv.weight": self.wqkv[i][qd + kd:], "attention.wo.weight": self.wo[i],
+                       "feed_forward.w1.weight": fused13[:, 0], "feed_forward.w3.weight": fused13[:, 1],
+                       "feed_forward.w2.weight": self.w2[i], "attention_norm.weight": self.attention_norm[i],
+                       "ffn_norm.weight": self.ffn_norm[i]}[rest]
+                if rest in ("feed_forward.w1.weight", "feed_forward.w3.weight"):
+                    t = t.reshape(h // 2, 2, c.dim)
+            dst.copy_(t.to(device=self.device, dtype=dst.dtype))
+
+    def _build(self, w):
+        """Allocate the device weights from a complete canonical-name dict and build
+        the fused layouts the kernels read: wq|wk|wv rows stacked, and w1 / w3
+        interleaved two rows at a time (rows 4j, 4j+1 = w1 rows 2j, 2j+1; rows
+        4j+2, 4j+3 = w3 rows 2j, 2j+1)."""
+        c = self.config
 
         def dev(name, dtype):
-            t = torch.as_tensor(w[name]) if not isinstance(w[name], torch.Tensor) else w[name]
-            if tuple(t.shape) != shapes[name]:
-                raise ValueError(f"{name}: shape {tuple(t.shape)} != {shapes[name]}")
-            return t.to(device=self.device, dtype=dtype).contiguous()
+            return w[name].to(device=self.device, dtype=dtype).contiguous()
 
         dt = c.dtype
         self.tok_embeddings = dev("tok_embeddings.weight", dt)
@@ -329,19 +372,49 @@ class Llama:
 
     def decode(self, tokens, kv_cache, block_manager, seq_ids, start_positions, block_tables_tensor,
                context_lens_tensor, jit_fn, max_blocks=64):
-        """Batched single-token decode (llama.py:346-388).  Returns logits [B, 1, vocab]."""
+        """Batched single-token decode (llama.py:346-388).  Returns logits [B, 1, vocab].
+
+        Each sequence's K/V go to the slot ``block_manager.get_slot(seq_id)``
+        names, as in the reference (llama.py:381-386): when the position starts a
+        new block, get_slot allocates it, although the engine built the tables
+        before that allocation (engine.py:152, 235-255).  The step computes the
+        write slot from the table, so the block is patched into the sequence's
+        row at column position // block_size.  Attention still covers the first
+        ``max_blocks`` columns only (llama.py:368-374); a position past them is
+        written through extra columns that attention does not read, as the
+        reference writes it to a block its truncated table does not list.
+        ``start_positions[i]`` must be the block manager's position of
+        ``seq_ids[i]`` (the engine passes ``len - 1``, engine.py:153), since the
+        reference rotates by the one and writes at the other.
+        """
         bt = _i32(block_tables_tensor, self.device)
+        if bt.dim() != 2:
+            raise ValueError("block_tables_tensor must be [batch, blocks]")
         batch = bt.shape[0]
-        if bt.shape[1] < max_blocks:                          # llama.py:368-374
-            bt = torch.cat([bt, torch.zeros((batch, max_blocks - bt.shape[1]), dtype=torch.int32,
-                                            device=self.device)], 1)
-        else:
-            bt = bt[:, :max_blocks]
-        graph = jit_fn.graph_for(kv_cache, batch, max_blocks)
-        graph.set_inputs(tokens, start_positions, context_lens_tensor, bt)
+        pos = [int(p) for p in np.asarray(start_positions).reshape(-1)]
+        if len(seq_ids) != batch or len(pos) != batch:
+            raise ValueError("seq_ids, start_positions and block_tables_tensor must have one entry per sequence")
+        bs = kv_cache.block_size
+        cols = []
+        for sid, p in zip(seq_ids, pos):
+            if block_manager.get_context_length(sid) != p:
+                raise ValueError(f"sequence {sid}: start position {p} is not the block manager's position "
+                                 f"{block_manager.get_context_length(sid)}")
+            _, block_id, _ = block_manager.get_slot(sid)      # llama.py:382 (allocates on a block boundary)
+            cols.append((p // bs, block_id))
+        need = max(c for c, _ in cols) + 1
+        width = max_blocks if need <= max_blocks else -(-need // 64) * 64
+        table = torch.zeros((batch, width), dtype=torch.int32, device=self.device)
+        n = min(bt.shape[1], max_blocks)                      # pad / truncate, llama.py:368-374
+        table[:, :n] = bt[:, :n]
+        rows = torch.arange(batch, device=self.device)
+        table[rows, torch.tensor([c for c, _ in cols], device=self.device)] = \
+            torch.tensor([b for _, b in cols], dtype=torch.int32, device=self.device)
+        graph = jit_fn.graph_for(kv_cache, batch, max_blocks, width)
+        graph.set_inputs(tokens, pos, context_lens_tensor, table)
         graph.step()
         logits = graph.logits.clone().unsqueeze(1)
-        for sid in seq_ids:                                   # llama.py:381-387
+        for sid in seq_ids:                                   # llama.py:387
             block_manager.advance_position(sid)
         return logits
 
@@ -354,12 +427,13 @@ class JitDecode:
         self.block_size = block_size
         self.graphs = {}
 
-    def graph_for(self, kv_cache, batch, max_blocks):
-        key = (id(kv_cache), batch, max_blocks)
+    def graph_for(self, kv_cache, batch, max_blocks, table_width=None):
+        width = max_blocks if table_width is None else table_width
+        key = (id(kv_cache), batch, max_blocks, width)
         if key not in self.graphs:
             if kv_cache.block_size != self.block_size:
                 raise ValueError("KV cache block size differs from the one the decode was created for")
-            self.graphs[key] = DecodeGraph(self.model, kv_cache, batch, max_blocks)
+            self.graphs[key] = DecodeGraph(self.model, kv_cache, batch, max_blocks, table_width=width)
         return self.graphs[key]
 
 
@@ -370,20 +444,27 @@ class DecodeGraph:
     buffers; each replay reads them, samples the next token into ``tokens`` and
     advances ``positions`` and ``context_lens`` by one, so ``run(n)`` decodes n
     tokens per sequence with no host work between steps (``history`` records
-    them when history_len > 0).
+    them when history_len > 0).  The tables are not extended on the device:
+    before ``run(n)`` every row must already list the blocks of positions up to
+    position + n - 1.  Attention reads the first ``max_blocks`` columns; the
+    K/V write slot of position p is column p // block_size of a row of
+    ``table_width`` (>= max_blocks) columns.
     """
 
-    def __init__(self, model, kv_cache, batch, max_blocks, *, partition_size=None, keep_logits=True,
-                 history_len=0):
+    def __init__(self, model, kv_cache, batch, max_blocks, *, table_width=None, partition_size=None,
+                 keep_logits=True, history_len=0):
         c = model.config
         dev = model.device
         self.model = model
         self.batch = batch
         self.max_blocks = max_blocks
+        self.table_width = max_blocks if table_width is None else int(table_width)
+        if self.table_width < max_blocks:
+            raise ValueError("table_width must be at least max_blocks")
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.positions = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.context_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
-        self.block_tables = torch.zeros((batch, max_blocks), dtype=torch.int32, device=dev)
+        self.block_tables = torch.zeros((batch, self.table_width), dtype=torch.int32, device=dev)
         self.logits = torch.zeros((batch, c.vocab_size), dtype=torch.float32, device=dev) if keep_logits else None
         self.history_len = history_len
         self.history = torch.zeros((batch, history_len), dtype=torch.int32, device=dev) if history_len else None
@@ -397,7 +478,7 @@ class DecodeGraph:
         self.workspace = torch.empty(need, dtype=torch.uint8, device=dev)
         self._cache, self._keep = model.cache_struct(kv_cache)
         self._args = _DecodeArgs(batch, self.tokens.data_ptr(), self.positions.data_ptr(),
-                                 self.context_lens.data_ptr(), self.block_tables.data_ptr(), max_blocks,
+                                 self.context_lens.data_ptr(), self.block_tables.data_ptr(), self.table_width,
                                  max_blocks, self.partition_size, 1 if model.write_before_attend else 0,
                                  self.logits.data_ptr() if self.logits is not None else None,
                                  self.history.data_ptr() if self.history is not None else None,
@@ -411,7 +492,14 @@ class DecodeGraph:
         self.tokens.copy_(_i32(tokens, dev).reshape(-1))
         self.positions.copy_(_i32(positions, dev).reshape(-1))
         self.context_lens.copy_(_i32(context_lens, dev).reshape(-1))
-        self.block_tables.copy_(_i32(block_tables, dev).reshape(self.batch, self.max_blocks))
+        bt = _i32(block_tables, dev).reshape(self.batch, -1)
+        if bt.shape[1] == self.table_width:
+            self.block_tables.copy_(bt)
+        elif bt.shape[1] == self.max_blocks:
+            self.block_tables.zero_()
+            self.block_tables[:, :self.max_blocks].copy_(bt)
+        else:
+            raise ValueError(f"block tables must have {self.max_blocks} or {self.table_width} columns")
 
     def step_eager(self):
         """Launch the step's kernels directly on the current stream."""
