@@ -98,6 +98,25 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * tv_paged_decode without a workspace argument: the split-context partials and
+ * the longest-first schedule live in a scratch array that the library holds on
+ * each device (16 MiB, allocated with the code object, kept until the process
+ * ends).  No counterpart in the reference; for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Arguments and results are those of tv_paged_decode
+ * with workspace = that scratch.  A launch whose tv_paged_decode_workspace_bytes
+ * exceeds 16 MiB fails with TV_EINVAL.  Allocates nothing; the first call on a
+ * device looks the scratch address up once.  All calls on one device share the
+ * scratch: calls that overlap on one device (different streams, or host
+ * threads) race and must be serialised by the caller.
+ */
+int tv_paged_decode_noalloc(void* out, const void* queries, const void* k_cache, const void* v_cache,
+                            const int32_t* block_tables, const int32_t* context_lens,
+                            int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                            int block_size, int num_blocks, int block_table_stride, int max_blocks,
+                            float scale, int dtype, int out_dtype, int partition_size, void* stream);
+
+/*
  * Prefill attention over one prompt.  Replaces flash_prefill_attention(...)
  * (tinyvllm/model/llama.py:58-94) with the batch dimension (always 1 there)
  * removed.  causal != 0 excludes key j for query i when j > i (top-left

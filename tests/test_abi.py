@@ -152,3 +152,13 @@ def test_decode_step_workspace_tinyllama():
     # 8 split partials of the widest product + activations + 500 x 64 argmax keys
     assert 64 * 2560 * 8 * 4 < ws < 16 << 20
     assert lib.tv_llama_decode_workspace_bytes(ctypes.byref(m), 0, 72, 16, 2048) == 0
+
+
+def test_noalloc_rejects_oversize_launch_on_the_host():
+    """tv_paged_decode_noalloc checks the launch against its 16 MiB per-device
+    scratch before any HIP call: a launch needing more fails with TV_EINVAL."""
+    lib = _lib.load()
+    assert lib.tv_paged_decode_workspace_bytes(64, 32, 128, 2048, 16, 256) > (16 << 20)
+    rc = lib.tv_paged_decode_noalloc(None, None, None, None, None, None, 64, 32, 8, 128, 16, 100, 2048, 2048,
+                                     0.1, _lib.TV_F16, _lib.TV_F16, 256, None)
+    assert rc == _lib.TV_EINVAL and b"scratch" in lib.tv_last_error()

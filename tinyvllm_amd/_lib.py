@@ -26,6 +26,7 @@ SIGNATURES = {
     "tv_paged_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),
     "tv_paged_decode_partition_size": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "tv_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P, _S, _P]),
+    "tv_paged_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P]),
     "tv_flash_prefill_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "tv_flash_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _L, _I, _F, _I, _I,
                               _I, _P, _S, _P]),
@@ -50,7 +51,7 @@ SIGNATURES = {
     "tv_llama_prefill_workspace_bytes": (_S, [_P, _I]),
     "tv_llama_prefill": (_I, [_P, _P, _P, _P]),
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 

@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <algorithm>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "../../include/tv_attn.h"
@@ -79,11 +80,47 @@ int vec_width(std::initializer_list<long long> sizes, std::initializer_list<cons
   return 2;
 }
 
+int paged_decode_impl(const char* who, void* out, const void* queries, const void* k_cache, const void* v_cache,
+                      const int32_t* block_tables, const int32_t* context_lens, int num_seqs, int num_heads,
+                      int num_kv_heads, int head_dim, int block_size, int num_blocks, int block_table_stride,
+                      int max_blocks, float scale, int dtype, int out_dtype, int partition_size, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+// Scratch of tv_paged_decode_noalloc: the split-context partials or the
+// longest-first schedule, in a file-scope device array instead of a caller's
+// workspace.  Every device the library runs on holds its own copy until the
+// process ends; the kernels fully write what they read back (no clearing).
+constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
+__device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device
+// (the host-side symbol is a stand-in, not a device address).
+int decode_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TV_EHIP, "tv_paged_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(TV_EINVAL, "tv_paged_decode_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TV_EHIP, "tv_paged_decode_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return TV_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int tv_abi_version(void) { return 6; }
+int tv_abi_version(void) { return 7; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
@@ -139,30 +176,68 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
                     int num_kv_heads, int head_dim, int block_size, int num_blocks, int block_table_stride,
                     int max_blocks, float scale, int dtype, int out_dtype, int partition_size, void* workspace,
                     size_t workspace_bytes, void* stream) {
+  return paged_decode_impl("tv_paged_decode", out, queries, k_cache, v_cache, block_tables, context_lens, num_seqs,
+                           num_heads, num_kv_heads, head_dim, block_size, num_blocks, block_table_stride, max_blocks,
+                           scale, dtype, out_dtype, partition_size, workspace, workspace_bytes, stream);
+}
+
+int tv_paged_decode_noalloc(void* out, const void* queries, const void* k_cache, const void* v_cache,
+                            const int32_t* block_tables, const int32_t* context_lens, int num_seqs, int num_heads,
+                            int num_kv_heads, int head_dim, int block_size, int num_blocks, int block_table_stride,
+                            int max_blocks, float scale, int dtype, int out_dtype, int partition_size, void* stream) {
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || block_size <= 0 || partition_size <= 0)
+    return fail(TV_EINVAL, "tv_paged_decode_noalloc: bad shape (num_seqs=%d, num_heads=%d, head_dim=%d, "
+                "max_blocks=%d, block_size=%d, partition_size=%d)", num_seqs, num_heads, head_dim, max_blocks,
+                block_size, partition_size);
+  const size_t need = tv_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, max_blocks, block_size,
+                                                      partition_size);
+  if (need > kDecodeScratchBytes)
+    return fail(TV_EINVAL, "tv_paged_decode_noalloc: the launch needs %zu bytes of scratch, more than the %zu the "
+                "library holds per device (use tv_paged_decode with a workspace, or larger partitions)",
+                need, (size_t)kDecodeScratchBytes);
+  void* scratch_ptr = nullptr;
+  if (need > 0) {
+    const int rc = decode_scratch(&scratch_ptr);
+    if (rc != TV_OK) return rc;
+  }
+  return paged_decode_impl("tv_paged_decode_noalloc", out, queries, k_cache, v_cache, block_tables, context_lens,
+                           num_seqs, num_heads, num_kv_heads, head_dim, block_size, num_blocks, block_table_stride,
+                           max_blocks, scale, dtype, out_dtype, partition_size, scratch_ptr, need, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int paged_decode_impl(const char* who, void* out, const void* queries, const void* k_cache, const void* v_cache,
+                      const int32_t* block_tables, const int32_t* context_lens, int num_seqs, int num_heads,
+                      int num_kv_heads, int head_dim, int block_size, int num_blocks, int block_table_stride,
+                      int max_blocks, float scale, int dtype, int out_dtype, int partition_size, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   if (!out || !queries || !k_cache || !v_cache || !block_tables || !context_lens)
-    return fail(TV_EINVAL, "tv_paged_decode: null pointer argument");
+    return fail(TV_EINVAL, "%s: null pointer argument", who);
   if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
-    return fail(TV_EINVAL, "tv_paged_decode: bad dtype %d / out_dtype %d", dtype, out_dtype);
+    return fail(TV_EINVAL, "%s: bad dtype %d / out_dtype %d", who, dtype, out_dtype);
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
-    return fail(TV_EINVAL, "tv_paged_decode: bad head counts (num_seqs=%d, num_heads=%d, num_kv_heads=%d)",
+    return fail(TV_EINVAL, "%s: bad head counts (num_seqs=%d, num_heads=%d, num_kv_heads=%d)", who,
                 num_seqs, num_heads, num_kv_heads);
   if (block_size <= 0 || num_blocks <= 0 || block_table_stride < 0 || max_blocks <= 0 ||
       (block_table_stride > 0 && max_blocks > block_table_stride))
-    return fail(TV_EINVAL, "tv_paged_decode: bad block geometry (block_size=%d, num_blocks=%d, stride=%d, max_blocks=%d)",
+    return fail(TV_EINVAL, "%s: bad block geometry (block_size=%d, num_blocks=%d, stride=%d, max_blocks=%d)", who,
                 block_size, num_blocks, block_table_stride, max_blocks);
   if ((long long)max_blocks * block_size > (1LL << 30))
-    return fail(TV_EINVAL, "tv_paged_decode: context width too large");
+    return fail(TV_EINVAL, "%s: context width too large", who);
   if (partition_size <= 0 || partition_size % 16 != 0)
-    return fail(TV_EINVAL, "tv_paged_decode: partition_size must be a positive multiple of 16 (got %d)",
+    return fail(TV_EINVAL, "%s: partition_size must be a positive multiple of 16 (got %d)", who,
                 partition_size);
   if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256))
-    return fail(TV_EUNSUPPORTED, "tv_paged_decode: head_dim %d not supported (16/32/64/128/256)", head_dim);
+    return fail(TV_EUNSUPPORTED, "%s: head_dim %d not supported (16/32/64/128/256)", who, head_dim);
   if (dtype != TV_F32 && head_dim < 16)
-    return fail(TV_EUNSUPPORTED, "tv_paged_decode: head_dim %d too small", head_dim);
+    return fail(TV_EUNSUPPORTED, "%s: head_dim %d too small", who, head_dim);
 
   if ((uintptr_t)out % 16 || (uintptr_t)queries % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
       (uintptr_t)block_tables % 4 || (uintptr_t)context_lens % 4)
-    return fail(TV_EINVAL, "tv_paged_decode: queries/caches/out must be 16-byte aligned");
+    return fail(TV_EINVAL, "%s: queries/caches/out must be 16-byte aligned", who);
 
   const int group = num_heads / num_kv_heads;
   const int gt = heads_per_group_chunk(group);
@@ -171,7 +246,7 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   const size_t need = tv_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, max_blocks, block_size,
                                                       partition_size);
   if (max_parts > 1 && (!workspace || workspace_bytes < need))
-    return fail(TV_EINVAL, "tv_paged_decode: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+    return fail(TV_EINVAL, "%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes);
   // the longest-first schedule is optional: without room for it the launch runs in batch order
   const bool ordered = max_parts == 1 && need > 0 && workspace && workspace_bytes >= need;
 
@@ -200,7 +275,7 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
     p.part_ml = p.part_o + n_o;
   }
   if (max_parts > 65535 || num_seqs > 65535 || num_kv_heads * p.head_chunks > 65535)
-    return fail(TV_EINVAL, "tv_paged_decode: grid too large");
+    return fail(TV_EINVAL, "%s: grid too large", who);
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   p.num_seqs = num_seqs;
@@ -221,13 +296,17 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
   if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, pair, grid, s);
   else if (dtype == TV_F16) launched = tv::launch_paged_decode<_Float16>(p, head_dim, gt, pair, grid, s);
   else launched = tv::launch_paged_decode<__bf16>(p, head_dim, gt, pair, grid, s);
-  if (!launched) return fail(TV_EUNSUPPORTED, "tv_paged_decode: no kernel for head_dim=%d gt=%d", head_dim, gt);
-  int rc = check_launch("tv_paged_decode");
+  if (!launched) return fail(TV_EUNSUPPORTED, "%s: no kernel for head_dim=%d gt=%d", who, head_dim, gt);
+  int rc = check_launch(who);
   if (rc != TV_OK || max_parts <= 1) return rc;
-  if (head_dim > 256) return fail(TV_EUNSUPPORTED, "tv_paged_decode: merge supports head_dim <= 256");
+  if (head_dim > 256) return fail(TV_EUNSUPPORTED, "%s: merge supports head_dim <= 256", who);
   hipLaunchKernelGGL(tv::paged_decode_reduce_kernel, dim3(num_heads, num_seqs), dim3(64), 0, s, p, head_dim);
-  return check_launch("tv_paged_decode(merge)");
+  return check_launch(who);
 }
+
+}  // namespace
+
+extern "C" {
 
 static void prefill_params(tv::PrefillParams& p, void* out, const void* q, const void* k, const void* v, int q_len,
                            int kv_len, int num_heads, int num_kv_heads, int head_dim, int head_dim_v,
