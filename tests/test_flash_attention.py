@@ -110,6 +110,21 @@ def test_mfma_path(dtype, d, lq, causal):
           randn(24, lq, hkv, d, dtype=dtype), causal)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("lq,hq,hkv", [(300, 8, 2), (1024, 32, 8)])
+def test_peaked_softmax(dtype, d, causal, lq, hq, hkv):
+    """q, k ~ N(0, 3^2): scores of tens of units, nearly one-hot softmax rows,
+    where any rounding of the scores (or of q * scale) before the softmax shows
+    up in the output.  The reference scales after the product (llama.py:84), in
+    fp32 here; bar: 2e-2 max-abs against the float64 oracle."""
+    q = randn(90, lq, hq, d) * 3
+    k = randn(91, lq, hkv, d) * 3
+    v = randn(92, lq, hkv, d)
+    check(q.to(dtype), k.to(dtype), v.to(dtype), causal)
+
+
 @pytest.mark.parametrize("length", [512, 1024])
 def test_tinyllama_prefill_shape(length):
     """TinyLlama prefill shape: Hq 32, Hkv 4, D 64, fp16 inputs, causal."""
@@ -228,6 +243,8 @@ def test_random_shapes(i, hq, hkv, d, lq, lk, causal, dtype, chunk):
     ([1, 17, 64, 300, 65], 8, 2, 64, True),    # ragged, single-token and tile-boundary prompts
     ([129, 7, 1000], 16, 8, 128, True),
     ([33, 200, 64], 8, 8, 64, False),
+    ([300, 41, 512], 8, 2, 64, True),          # <= 256 work-groups with long rows: two key groups + LDS merge
+    ([300, 41, 512], 8, 2, 128, True),
 ])
 def test_varlen_matches_per_prompt(lens, hq, hkv, d, causal, dtype):
     """Every prompt of a packed batch equals the oracle on that prompt alone and

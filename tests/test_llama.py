@@ -509,7 +509,8 @@ def test_tinyllama_shape_matches_oracle():
         logits = model.decode(torch.tensor(nxt).reshape(-1, 1), kv, bm, [0, 1, 2], pos, torch.from_numpy(bt),
                               torch.tensor(ctx, dtype=torch.int32), jit, 2)
         want = ref.decode(nxt, pos, ctx, bt, rk, rv, 16)
-        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        err = max_err(logits[:, 0].cpu().numpy(), want)
+        assert err < TOL, (step, err)
         top2 = np.sort(want, axis=1)[:, -2:]
         clear = top2[:, 1] - top2[:, 0] > 2 * TOL
         got_tok = logits[:, 0].cpu().numpy().argmax(1)
@@ -558,7 +559,8 @@ def test_decode_allocates_the_new_block_like_get_slot(write_before_attend):
         assert after == [b + (p % 16 == 0 and p // 16 == b) for b, p in zip(before, pos)], step
         full = engine_tables(bm, seqs, max_blocks)
         want = ref.decode(toks, pos, ctx, full, rk, rv, 16, write_before_attend=write_before_attend)
-        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        err = max_err(logits[:, 0].cpu().numpy(), want)
+        assert err < TOL, (step, err)
         assert [bm.get_context_length(s) for s in seqs] == [p + 1 for p in pos]
         toks = [int(t) for t in greedy_ref(want)]
     assert all(0 not in bm.get_block_table(s) for s in seqs)
@@ -586,7 +588,8 @@ def test_decode_past_the_table_width_writes_kv_and_truncates_attention():
                               torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
         full = engine_tables(bm, [0, 1], 3)
         want = ref.decode(toks, pos, ctx, full, rk, rv, 16, max_blocks=max_blocks)
-        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        err = max_err(logits[:, 0].cpu().numpy(), want)
+        assert err < TOL, (step, err)
         toks = [int(t) for t in greedy_ref(want)]
     check_caches(kv, rk, rv)
     slot = bm.get_block_table(0)[41 // 16] * 16 + 41 % 16
@@ -620,7 +623,13 @@ def test_decode_block_sizes_match_oracle(ctx_convention, block_size, dtype):
                               torch.tensor(ctx, dtype=torch.int32), jit, max_blocks)
         assert logits.shape == (3, 1, cfg.vocab_size) and not logits.isnan().any()
         want = ref.decode(toks, pos, ctx, bt, rk, rv, block_size)
-        assert max_err(logits[:, 0].cpu().numpy(), want) < TOL, step
+        err = max_err(logits[:, 0].cpu().numpy(), want)
+        # A bf16 model stores its activations (normalised x, q/k/v, attention
+        # output, SwiGLU output) with 8 significant bits, which moves logits by
+        # about 1% of their scale on its own: bf16 logits are held to 2e-2 of
+        # the logit scale, fp16 logits to 2e-2 absolute.
+        tol = TOL * max(1.0, float(np.abs(want).max())) if dtype == "bfloat16" else TOL
+        assert err < tol, (step, err, tol)
         toks = [int(t) for t in greedy_ref(want)]
     check_caches(kv, rk, rv)
 

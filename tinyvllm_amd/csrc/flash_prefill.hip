@@ -91,11 +91,11 @@ __device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v, int out_
 // A work-group owns 64 query rows of one head.  KS groups of QW = 4 / RB waves
 // split the row block's BN-key tiles (group s takes tiles s + KS j of its key
 // range); every wave owns RB blocks of 16 query rows, so each K / V fragment
-// read from LDS feeds RB matrix products.  Per tile a wave computes S^T = K Q^T with
-// Q pre-scaled by scale * log2(e) and the accumulator initialised to -m (the
-// running reference maximum of the query), so the scores come out of the
-// matrix cores already in the log2 domain relative to m and go straight into
-// v_exp_f32.  m is raised only when a tile exceeds it by more than 8, which
+// read from LDS feeds RB matrix products.  Per tile a wave computes S^T = K Q^T
+// and brings the scores into the log2 domain relative to m, the running
+// reference maximum of the query (for fp16 inside the matrix cores, with Q
+// pre-scaled and the accumulator initialised to -m; for bf16 with one fp32 fma
+// per score, see kPreScaleQ), so they go straight into v_exp_f32.  m is raised only when a tile exceeds it by more than 8, which
 // after the first tile is rare.  V is staged row-major in LDS and read as
 // the V^T operand with ds_read_b64_tr_b16; the softmax row sums come from one
 // extra MFMA of P against a register of ones.  Tiles are double-buffered in LDS
@@ -112,6 +112,18 @@ template <typename T> __device__ __forceinline__ u32x4 scale8(u32x4 w, float c) 
   }
   return r;
 }
+
+// Where the softmax scale enters.  fp16: Q is pre-scaled by scale * log2(e)
+// and rounded to fp16 once (a relative error of at most 2^-11 per element,
+// comparable to the rounding of the fp16 inputs themselves), and the score
+// accumulator starts at -m, so scores leave the matrix cores ready for exp2.
+// bf16: rounding q * scale to bf16 would add up to 2^-8 relative error to
+// every score (scores of tens of units then move the softmax by several
+// percent), so Q stays as given, the accumulator starts at 0 and each score
+// takes one fp32 fma, s * scale * log2(e) - m -- the reference's order, the
+// scale applied after the product (llama.py:84).
+template <typename T> constexpr bool kPreScaleQ = false;
+template <> constexpr bool kPreScaleQ<_Float16> = true;
 
 template <typename T> constexpr uint32_t kOnes2 = 0;
 template <> constexpr uint32_t kOnes2<_Float16> = 0x3C003C00u;
@@ -213,10 +225,11 @@ prefill_fa_kernel(const PrefillParams pa) {
     for (int r = 0; r < RB; ++r) {
       qi[r] = row0 + r * 16 + col;
 #pragma unroll
-      for (int ks = 0; ks < KSD; ++ks)
-        qf[r][ks] = qi[r] < p.q_len
-                        ? scale8<T>(*reinterpret_cast<const u32x4*>(qg + (size_t)qi[r] * p.q_stride + ks * 32 + g * 8), c)
-                        : u32x4{0, 0, 0, 0};
+      for (int ks = 0; ks < KSD; ++ks) {
+        const u32x4 raw = qi[r] < p.q_len ? *reinterpret_cast<const u32x4*>(qg + (size_t)qi[r] * p.q_stride + ks * 32 + g * 8)
+                                          : u32x4{0, 0, 0, 0};
+        qf[r][ks] = kPreScaleQ<T> ? scale8<T>(raw, c) : raw;
+      }
     }
   }
 
@@ -297,6 +310,14 @@ prefill_fa_kernel(const PrefillParams pa) {
 #pragma unroll
         for (int ks = 1; ks < KSD; ++ks) st[r][kb] = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], st[r][kb]);
       }
+    if constexpr (!kPreScaleQ<T>) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[r][kb][i] = fmaf(st[r][kb][i], c, -mref[r]);
+    }
     // V^T fragments: rows (keys) ks2*32 + 4g + (col >> 2) (+16), columns db*16 + 4 (col & 3)
     u32x4 vf[DB][BN / 32];
 #pragma unroll
@@ -346,7 +367,7 @@ prefill_fa_kernel(const PrefillParams pa) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) st[r][kb] -= delta;
         mref[r] += delta;
-        negm[r] = f32x4{-mref[r], -mref[r], -mref[r], -mref[r]};
+        if constexpr (kPreScaleQ<T>) negm[r] = f32x4{-mref[r], -mref[r], -mref[r], -mref[r]};
         thr[r] = need ? 8.0f : thr[r];
       }
     }
