@@ -33,7 +33,7 @@ CFLAGS = [
 # Per-file flags.  The prefill kernels take maxima of scores that come out of
 # the matrix cores and are never NaN for finite inputs; without NaN semantics
 # the compiler emits v_max3 trees without canonicalising every operand.
-FILE_FLAGS = {"flash_prefill.hip": ["-fno-honor-nans"]}
+FILE_FLAGS = {"flash_prefill.hip": ["-fno-honor-nans"], "flash_prefill_rows.hip": ["-fno-honor-nans"]}
 
 
 def _compile(src: Path) -> Path:

@@ -668,6 +668,22 @@ template <typename T, int D> void launch_fa(int cfg, dim3 grid, const PrefillPar
 #endif
 }
 
+// 128-row work-groups with LDS-DMA tiles (prefill_rows_kernel,
+// flash_prefill_rows.hip) for long head_dim-128 prompts, where they measured
+// faster (MI355X, Hq 32 / Hkv 8: L 2048 62-64 against 64-68 us, L 4096
+// 178-185 against 207-210); below 2048 rows, or at head_dim 64, this file's
+// 64-row kernel wins.
+#ifndef TV_PREFILL_ROWS_MODE
+#define TV_PREFILL_ROWS_MODE 1     // 0: never, 1: long head_dim-128 prompts, 2: always (when the shape allows)
+#endif
+constexpr int kRowsMinLen = 2048;
+
+bool use_rows_kernel(int head_dim, long long max_q_len) {
+  if (TV_PREFILL_ROWS_MODE == 0) return false;
+  if (TV_PREFILL_ROWS_MODE == 2) return true;
+  return head_dim == 128 && max_q_len >= kRowsMinLen;
+}
+
 // Returns 0 on launch, 1 if the shape has no kernel, 2 if the workspace is missing.
 int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, size_t workspace_bytes,
                          hipStream_t stream) {
@@ -677,6 +693,9 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     int units, max_chunks;
     prefill_units(pp, units, max_chunks);
     pp.max_chunks = max_chunks;
+    if (max_chunks == 1 && use_rows_kernel(pp.head_dim, pp.q_len) &&
+        launch_prefill_rows(pp, dtype, 1, pp.q_len, stream))
+      return 0;
     if (max_chunks > 1) {
       const size_t need = prefill_workspace_bytes(pp, dtype);
       if (!workspace || workspace_bytes < need) return 2;
@@ -734,6 +753,9 @@ int launch_flash_prefill_varlen(const PrefillParams& p_in, int num_seqs, int max
   pp.max_chunks = 1;
   pp.part_o = nullptr;
   pp.part_ml = nullptr;
+  if (use_rows_kernel(pp.head_dim, max_q_len) &&
+      launch_prefill_rows(pp, dtype, num_seqs, max_q_len, stream))
+    return 0;
   const int nqt = (max_q_len + kPrefillBM - 1) / kPrefillBM;
   const dim3 grid(pp.num_heads, nqt, num_seqs);
   const long long wgs = (long long)pp.num_heads * ((total_q + kPrefillBM - 1) / kPrefillBM + num_seqs);

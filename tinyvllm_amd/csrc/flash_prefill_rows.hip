@@ -1,0 +1,376 @@
+// Causal / full prefill attention for large grids: 128 query rows per
+// work-group, 32 per wave, K/V tiles loaded straight into LDS.
+//
+// Same semantics as prefill_fa_kernel (flash_prefill.hip; reference
+// tinyvllm/model/llama.py:58-94): scores (q.k)*scale, key j excluded for query
+// i when j > i with `causal` (top-left aligned), query head h on KV head
+// h / (Hq/Hkv), fp16 / bf16 inputs, fp32 accumulation, head_dim 64 or 128.
+//
+// Why a second kernel.  In the 64-row kernel every wave owns 16 query rows, so
+// each K / V byte read from LDS feeds 16 rows of MFMA work: at full matrix
+// rate a CU would need ~256 B/clk of LDS reads, all the LDS has, and every
+// tile also passes through VGPRs and ds_write_b128 on its way in.  Here:
+//  * a wave owns 32 query rows (two 16-row blocks), so every K / V fragment
+//    read from LDS feeds two MFMAs -- half the LDS read traffic per FLOP;
+//  * the four waves of a work-group (128 rows) share each staged tile;
+//  * tiles arrive by buffer_load_dwordx4 ... lds (each lane's 16 bytes land at
+//    M0 + 16 * lane): no staging registers, no LDS write instructions;
+//  * since such a load writes 1 KB contiguously, rows are not padded; instead
+//    the 16-byte chunks of row r are XOR-permuted (chunk c at slot c ^ f(r)),
+//    chosen so that both the 16-row K fragment reads (ds_read_b128) and the
+//    transposing V reads (ds_read_b64_tr_b16) touch distinct banks;
+//  * four tile buffers: tile j + 3 is requested while tile j is consumed, one
+//    barrier per tile.
+// The softmax is the 64-row kernel's: log2 domain, lazy rescale (threshold 8),
+// P kept in registers as the B operand of O^T = V^T P^T; the scale is applied
+// in fp32 after the product, s * scale * log2(e) - m in one fma (llama.py:84).
+// Row sums of the rounded P accumulate per lane with v_dot2 against ones (VALU,
+// instead of an extra MFMA per tile) and are summed over the four lanes of a
+// query at the end.
+//
+// Measured on MI355X (Llama-3-8B heads, Hq 32 / Hkv 8, head_dim 128, fp16,
+// causal): L 2048 62-64 us against 64-68 for the 64-row kernel, L 4096 178-185
+// against 207-210; at L <= 1024 and at head_dim 64 the 64-row kernel is faster
+// (more, shorter work-groups), so the launcher uses this one only for long
+// head_dim-128 prompts.  A tile step of the longest work-group takes ~2000
+// cycles against 512 of MFMA work (clock stamps): the LDS-DMA issue, LDS read
+// issue, score wait and softmax are serial within a wave, and with 2 waves per
+// SIMD (208 VGPRs) little of it overlaps.  Splitting a work-group's key tiles
+// over two 4-wave groups in ping-pong (one group's MFMA phase against the
+// other's softmax phase, a barrier per phase) was correct but 2x slower: the
+// softmax phase of one wave ran ~4x longer while the other issued MFMAs.
+#include "tv_common.h"
+#include "tv_params.h"
+
+#include <type_traits>
+
+namespace tv {
+
+namespace {
+
+constexpr int kRowsBM = 128;   // query rows per work-group
+constexpr int kRowsBN = 32;    // keys per tile
+constexpr int kRowsBuf = 4;    // tile buffers
+
+// chunk permutation of tile row r (16-byte chunks; 16 per row at head_dim 128,
+// 8 at 64): distinct over any 16 consecutive rows for a fixed chunk (K reads),
+// and keeps the chunk pairs {2u, 2u+1} of 4 consecutive rows on distinct banks
+// (transposing V reads).
+template <int D> __device__ __forceinline__ int chunk_perm(int r) {
+  if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+}
+
+// 16 bytes per lane from buffer `rsrc` at byte offset voff straight into LDS at
+// lds_base + 16 * lane (gfx950 LDS DMA).  The compiler does not see these
+// loads: callers wait for them with wait_vmcnt before a barrier.
+__device__ __forceinline__ void load_lds16(u32x4 rsrc, uint32_t lds_base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ uint32_t sgpr(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, unsigned long long bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  const uint32_t n = bytes >> 32 ? 0xffffffffu : (uint32_t)bytes;
+  return u32x4{sgpr((uint32_t)a), sgpr((uint32_t)(a >> 32)), sgpr(n), 0x00020000u};
+}
+
+template <typename T> constexpr uint32_t kRowsOnes2 = 0;
+template <> constexpr uint32_t kRowsOnes2<_Float16> = 0x3C003C00u;
+template <> constexpr uint32_t kRowsOnes2<__bf16> = 0x3F803F80u;
+
+// acc + the sum of the eight packed 16-bit values of p (fp32 accumulation)
+template <typename T> __device__ __forceinline__ float rowsum8(u32x4 p, float acc) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) acc = dot2<T>(p[w], kRowsOnes2<T>, acc);
+  return acc;
+}
+
+}  // namespace
+
+// Query tile of unit u, zig-zag: the longer half of the causal tiles longest
+// first, then the shorter half shortest first.
+__device__ __forceinline__ int rows_unit_tile(int u, int nqt) {
+  const int half = (nqt + 1) / 2;
+  return u < half ? nqt - 1 - u : u - half;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+prefill_rows_kernel(const PrefillParams pa) {
+  PrefillParams p = pa;
+  if (pa.cu_q) {
+    const int z = pa.seq_order ? pa.seq_order[blockIdx.z] : (int)blockIdx.z;
+    const int q0 = pa.cu_q[z], k0 = pa.cu_k[z];
+    p.q_len = pa.cu_q[z + 1] - q0;
+    p.kv_len = pa.cu_k[z + 1] - k0;
+    if ((int)blockIdx.y * kRowsBM >= p.q_len || p.kv_len <= 0) return;
+    p.q = reinterpret_cast<const T*>(pa.q) + (size_t)q0 * pa.q_stride;
+    p.k = reinterpret_cast<const T*>(pa.k) + (size_t)k0 * pa.k_stride;
+    p.v = reinterpret_cast<const T*>(pa.v) + (size_t)k0 * pa.v_stride;
+    p.out = reinterpret_cast<char*>(pa.out) + (size_t)q0 * pa.out_stride * (pa.out_dtype == kF32 ? 4 : 2);
+  }
+  constexpr int BM = kRowsBM, BN = kRowsBN, NB = kRowsBuf;
+  constexpr int RB = 2;                    // 16-row blocks per wave
+  constexpr int KB = BN / 16;              // 16-key blocks per tile
+  constexpr int KSD = D / 32;              // MFMA steps over the head dim
+  constexpr int DB = D / 16;               // 16-dim blocks of O^T
+  constexpr int ROWB = 2 * D;              // bytes per tile row
+  constexpr int TILEB = BN * ROWB;         // bytes of the K (or V) tile
+  constexpr int BUFB = 2 * TILEB;          // one K + V buffer
+  constexpr int NI = TILEB / 1024 / 4;     // LDS-DMA instructions per wave per tile, each of K and V
+  constexpr int RPI = 1024 / ROWB;         // tile rows per DMA instruction
+  constexpr int SPR = ROWB / 16;           // 16-byte chunks per row
+  static_assert(NI >= 1 && NI * 4 * 1024 == TILEB, "tile / DMA shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NB * BUFB];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int col = lane & 15;
+
+  const int h = p.xcd_remap ? ((int)(blockIdx.x & 7) * (p.num_heads >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
+  const int nqt = (p.q_len + BM - 1) / BM;
+  const int qt = rows_unit_tile(blockIdx.y, nqt);
+  const int kvh = h / (p.num_heads / p.num_kv_heads);
+  const int klim = p.kv_len;
+  const int kend = p.causal ? min(klim, (qt + 1) * BM) : klim;
+  const int ntiles = (kend + BN - 1) / BN;
+  const float c = p.scale * kLog2e;
+  const int row0 = qt * BM + wave * 32;    // first query row of this wave
+
+  // ---- Q fragments (B operand of S^T = K Q^T) ----
+  int qi[RB];
+  u32x4 qf[RB][KSD];
+  {
+    const T* qg = reinterpret_cast<const T*>(p.q) + (size_t)h * D;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      qi[r] = row0 + r * 16 + col;
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks) {
+        qf[r][ks] = qi[r] < p.q_len
+                        ? *reinterpret_cast<const u32x4*>(qg + (size_t)qi[r] * p.q_stride + ks * 32 + g * 8)
+                        : u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+
+  // ---- LDS-DMA addressing: wave w loads instructions w*NI .. w*NI+NI-1 of each tile ----
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const char* kbase = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.k) + (size_t)kvh * D);
+  const char* vbase = reinterpret_cast<const char*>(reinterpret_cast<const T*>(p.v) + (size_t)kvh * D);
+  const unsigned long long kstr = (unsigned long long)p.k_stride * sizeof(T);
+  const unsigned long long vstr = (unsigned long long)p.v_stride * sizeof(T);
+  uint32_t kvoff[NI], vvoff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = (wave * NI + i) * RPI + lane / SPR;
+    const int slot = lane % SPR;
+    const int chunk = slot ^ chunk_perm<D>(row);
+    kvoff[i] = (uint32_t)(row * kstr + chunk * 16);
+    vvoff[i] = (uint32_t)(row * vstr + chunk * 16);
+  }
+  // tile t (clamped to the last tile) into buffer t % NB; the resource's range
+  // ends at the last key row
+  auto issue = [&](int t) {
+    const int tc = min(t, ntiles - 1);
+    const unsigned long long r0 = (unsigned long long)tc * BN;
+    const unsigned long long kb = ((unsigned long long)(klim - 1) - r0) * kstr + D * sizeof(T);
+    const unsigned long long vb = ((unsigned long long)(klim - 1) - r0) * vstr + D * sizeof(T);
+    const u32x4 rk = rsrc_words(kbase + r0 * kstr, kb);
+    const u32x4 rv = rsrc_words(vbase + r0 * vstr, vb);
+    const uint32_t buf = lds0 + (uint32_t)((t % NB) * BUFB);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) load_lds16(rk, sgpr(buf + (uint32_t)((wave * NI + i) * 1024)), kvoff[i]);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) load_lds16(rv, sgpr(buf + (uint32_t)(TILEB + (wave * NI + i) * 1024)), vvoff[i]);
+  };
+
+  // The Q loads are the only global loads the compiler tracks; retire them
+  // here so its own wait for them cannot land inside the tile loop (where it
+  // would also drain the LDS-DMA loads in flight).
+  wait_vmcnt<0>();
+  // Rows past kv_len read as zero through the resource range; the buffers start
+  // zeroed so nothing non-finite can reach a masked product.
+  for (int i = threadIdx.x; i < NB * BUFB / 16; i += 256) reinterpret_cast<u32x4*>(smem)[i] = u32x4{0, 0, 0, 0};
+  lds_barrier();
+  issue(0);
+  issue(1);
+  issue(2);
+
+  // fragment read offsets inside a buffer (bytes).  chunk_perm(r + 16) ==
+  // chunk_perm(r), so the second 16-key block and the upper 16 V rows are the
+  // same offsets plus a constant.  K chunk 4 ks + g of row col sits at slot
+  // ((ks ^ fk) << 2) | (g ^ (f & 3)) with f = chunk_perm(col), fk = f >> 2; V
+  // chunk 2 db + b of row r at ((db ^ fv) << 1) | (b ^ (f_r & 1)), fv = f_r >> 1:
+  // one base and one XOR key per operand instead of a register per offset.
+  const int kperm = chunk_perm<D>(col);
+  const int kofs0 = col * ROWB + ((g ^ (kperm & 3)) << 4);
+  const int kkey = kperm >> 2;
+  auto koff = [&](int ks) { return kofs0 + ((ks ^ kkey) << 6); };
+  const int vrow = 4 * g + (col >> 2);
+  const int vperm = chunk_perm<D>(vrow);
+  const int vofs0 = TILEB + vrow * ROWB + ((((col & 3) >> 1) ^ (vperm & 1)) << 4) + 8 * (col & 1);
+  const int vkey = vperm >> 1;
+  auto voff = [&](int db) { return vofs0 + ((db ^ vkey) << 5); };
+
+  f32x4 oacc[RB][DB];
+  float lpart[RB];      // this lane's share of the row sum (keys 4g..4g+3 of every 16)
+  float mref[RB], thr[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[r][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    lpart[r] = 0.0f;
+    mref[r] = 0.0f;
+    thr[r] = -__FLT_MAX__;
+  }
+
+  // raw scores of a tile starting at key k0 -> log2 domain relative to the
+  // running maximum (one fma), masked, rescaled when a row's maximum moved by
+  // more than 8
+  auto softmax = [&](f32x4 (&st)[RB][KB], int k0) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[r][kb][i] = fmaf(st[r][kb][i], c, -mref[r]);
+    if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0))) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int rel = (p.causal ? min(klim - 1, qi[r]) : klim - 1) - (k0 + 4 * g);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[r][kb][i] = kb * 16 + i <= rel ? st[r][kb][i] : kNegInf;
+      }
+    }
+    float lm[RB];
+    bool need_any = false;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      float t0 = fmaxf(fmaxf(st[r][0][0], st[r][0][1]), fmaxf(st[r][0][2], st[r][0][3]));
+#pragma unroll
+      for (int kb = 1; kb < KB; ++kb)
+        t0 = fmaxf(t0, fmaxf(fmaxf(st[r][kb][0], st[r][kb][1]), fmaxf(st[r][kb][2], st[r][kb][3])));
+      lm[r] = t0;
+      need_any = need_any || lm[r] > thr[r];
+    }
+    if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const float mt = max_over_g(lm[r]);
+        const bool need = mt > thr[r];
+        const float delta = need ? mt : 0.0f;
+        const float alpha = need && thr[r] > 0.0f ? fast_exp2(-delta) : 1.0f;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[r][db] *= alpha;
+        lpart[r] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) st[r][kb] -= delta;
+        mref[r] += delta;
+        thr[r] = need ? 8.0f : thr[r];
+      }
+    }
+  };
+
+  const bool idle = row0 >= p.q_len;       // rows past the prompt: nothing to compute
+  auto step = [&](auto bufc, int jj) {
+    constexpr int B = decltype(bufc)::value;
+    wait_vmcnt<4 * NI>();        // this wave's loads of tile jj are in LDS (tiles jj+1, jj+2 may fly)
+    lds_barrier();               // every wave's; and every wave is done with tile jj-1's buffer
+    issue(jj + 3);
+    const int k0 = jj * BN;
+    if (idle || (p.causal && k0 > row0 + 31)) return;   // nothing visible in the tile
+    const uint8_t* sb = smem + B * BUFB;
+
+    u32x4 kf[KB][KSD];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < KSD; ++ks) kf[kb][ks] = *reinterpret_cast<const u32x4*>(sb + koff(ks) + kb * 16 * ROWB);
+    f32x4 st[RB][KB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        st[r][kb] = mfma16x16x32<T>(kf[kb][0], qf[r][0], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int ks = 1; ks < KSD; ++ks) st[r][kb] = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], st[r][kb]);
+      }
+    u32x4 vf[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(sb + voff(db)));
+      const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(sb + voff(db) + 16 * ROWB));
+      vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+    softmax(st, k0);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      // reduction index 8g + j: key 4g + j of block 0 (j < 4), 4g + j - 4 of block 1
+      const u32x4 pf = u32x4{pack2<T>(fast_exp2(st[r][0][0]), fast_exp2(st[r][0][1])),
+                             pack2<T>(fast_exp2(st[r][0][2]), fast_exp2(st[r][0][3])),
+                             pack2<T>(fast_exp2(st[r][1][0]), fast_exp2(st[r][1][1])),
+                             pack2<T>(fast_exp2(st[r][1][2]), fast_exp2(st[r][1][3]))};
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[r][db] = mfma16x16x32<T>(vf[db], pf, oacc[r][db]);
+      lpart[r] = rowsum8<T>(pf, lpart[r]);
+    }
+  };
+  for (int jj = 0; jj < ntiles; jj += NB) {    // unrolled over the buffers: LDS offsets are constants
+    step(std::integral_constant<int, 0>{}, jj);
+    if (jj + 1 < ntiles) step(std::integral_constant<int, 1>{}, jj + 1);
+    if (jj + 2 < ntiles) step(std::integral_constant<int, 2>{}, jj + 2);
+    if (jj + 3 < ntiles) step(std::integral_constant<int, 3>{}, jj + 3);
+  }
+  wait_vmcnt<0>();               // the clamped trailing loads land before the work-group ends
+
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const float lsum = sum_over_g(lpart[r]);
+    if (qi[r] >= p.q_len) continue;
+    const float inv = 1.0f / lsum;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const size_t idx = (size_t)qi[r] * p.out_stride + (size_t)h * D + db * 16 + 4 * g;
+      const f32x4 v = oacc[r][db] * inv;
+      if (p.out_dtype == kF32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + idx) = v;
+      } else {
+        const u32x2 w = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + idx) = w;
+      }
+    }
+  }
+}
+
+// Launch for one prompt (grid.z = 1) or several (cu_q set; grid.z = prompts).
+// Returns false when the shape is not handled here.
+bool launch_prefill_rows(const PrefillParams& pp, int dtype, int num_seqs, int max_q_len, hipStream_t stream) {
+  if (!(dtype == kF16 || dtype == kBF16) || !(pp.head_dim == 64 || pp.head_dim == 128)) return false;
+  const dim3 grid(pp.num_heads, (max_q_len + kRowsBM - 1) / kRowsBM, num_seqs);
+  if (dtype == kF16) {
+    if (pp.head_dim == 64) hipLaunchKernelGGL((prefill_rows_kernel<_Float16, 64>), grid, dim3(256), 0, stream, pp);
+    else hipLaunchKernelGGL((prefill_rows_kernel<_Float16, 128>), grid, dim3(256), 0, stream, pp);
+  } else {
+    if (pp.head_dim == 64) hipLaunchKernelGGL((prefill_rows_kernel<__bf16, 64>), grid, dim3(256), 0, stream, pp);
+    else hipLaunchKernelGGL((prefill_rows_kernel<__bf16, 128>), grid, dim3(256), 0, stream, pp);
+  }
+  return true;
+}
+
+}  // namespace tv

@@ -70,6 +70,7 @@ bool prefill_uses_mfma(const PrefillParams& p, int dtype);
 size_t prefill_workspace_bytes(const PrefillParams& p, int dtype);
 int launch_flash_prefill(const PrefillParams& p, int dtype, void* workspace, size_t workspace_bytes,
                          hipStream_t stream);
+bool launch_prefill_rows(const PrefillParams& p, int dtype, int num_seqs, int max_q_len, hipStream_t stream);
 int launch_flash_prefill_varlen(const PrefillParams& p, int num_seqs, int max_q_len, int max_kv_len,
                                 long long total_q, int dtype, hipStream_t stream);
 void launch_kv_write(const KVWriteParams& p, int vec_bytes, hipStream_t stream);
