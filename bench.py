@@ -14,10 +14,14 @@ random-init TinyLlama-1.1B at batch 64 / context 1024 (tok/s over 128 steps).
 Timing: W warm-up launches, then K launches back to back bracketed by
 torch.cuda.synchronize() and HIP events on the stream the kernels run on
 (torch's current stream).  Small workloads are captured in a HIP graph of K
-launches so launch overhead is not measured.  ``cpu_baseline`` times the
-oracle's float32 restatement of the reference algorithm (padded gather, GQA
-expand, full scores, -1e9 mask, softmax, PV; llama.py:97-144) on the host for a
-bounded sample of the primary workload.
+launches so launch overhead is not measured.  Every workload carries a
+``cpu_baseline``: the oracle's float32 numpy restatement of the reference
+algorithm (CPU restatement, tinygrad unavailable) timed on the host cores on a
+bounded sample -- the padded-gather decode (llama.py:97-144), the full L x L
+prefill and per-chunk K/V write loop (llama.py:58-94, 199-209), and one batched
+decode step of the model (llama.py:290-388), whose logits also check the GPU's
+step 1.  ``traffic`` figures come from rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+recorded under profiles/.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -43,6 +47,12 @@ FP16_PEAK_TFLOPS = 2500.0
 # profiles/paged_decode_llama3_8b_f16.md.
 PRIMARY_TRAFFIC_BYTES = 2500746870
 PRIMARY_TRAFFIC_SOURCE = "profiles/paged_decode_llama3_8b_f16.md"
+# The same measurement for the split-context decode (decode + merge, per
+# launch) and for one TinyLlama decode step (all 157 launches, context 1024).
+LONG_TRAFFIC_BYTES = 2152432806
+LONG_TRAFFIC_SOURCE = "profiles/paged_decode_long_bf16_b16.md"
+STEP_TRAFFIC_BYTES = 4220932722
+STEP_TRAFFIC_SOURCE = "profiles/decode_step_tinyllama_b64.md"
 
 
 def log(msg):
@@ -79,45 +89,148 @@ def timed(fn, steps, warmup, graph=False):
     return start.elapsed_time(end) / steps
 
 
-def cpu_baseline_decode(wl, seconds=10.0, sample_seqs=16):
-    """Time the oracle's fp32 restatement of the reference on a sample of sequences."""
+CPU_LABEL = "CPU restatement, tinygrad unavailable"
+
+
+def cpu_env():
+    """Host threads the CPU baselines run on: numpy's BLAS pool (matrix products)
+    and the process's CPU set; elementwise numpy work runs on one thread."""
+    import numpy  # noqa: F401  (loads the BLAS library threadpoolctl inspects)
+    from threadpoolctl import threadpool_info
+    blas = [p for p in threadpool_info() if p.get("user_api") == "blas"]
+    return {"blas_threads": max((int(p["num_threads"]) for p in blas), default=1),
+            "blas": blas[0].get("internal_api", "?") if blas else "none",
+            "sched_getaffinity": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count()}
+
+
+def _cpu_entry(value, unit, sample, env, **extra):
+    out = {"value": value, "unit": unit, "cores": env["blas_threads"], "kind": "port", "label": CPU_LABEL,
+           "sample": sample, "threads": {**env, "note": "BLAS products on blas_threads threads; "
+                                                            "elementwise numpy on one thread"}}
+    out.update(extra)
+    return out
+
+
+def _time_cpu(fn, seconds, min_iters=1):
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= min_iters:
+            return n, el
+
+
+def _compact_decode(wl, idx):
+    """q, caches and remapped tables of the sequences ``idx`` of a decode workload, on the host."""
     import torch
-    from oracle.attention import paged_decode_ref
-    idx = np.arange(min(sample_seqs, wl.batch))
     bt = wl.block_tables[idx]
-    ctx = wl.context_lens[idx]
     used = sorted(set(bt.reshape(-1).tolist()))
     remap = {b: i for i, b in enumerate(used)}
     bt_s = np.vectorize(remap.get)(bt).astype(np.int32)
     sel = torch.tensor(used, dtype=torch.long, device=wl.k_cache.device)
     kc = wl.k_cache.index_select(0, sel).float().cpu().numpy()
     vc = wl.v_cache.index_select(0, sel).float().cpu().numpy()
-    q = wl.q[idx.tolist()].float().cpu().numpy()
-    n, t0 = 0, time.perf_counter()
-    while True:
-        paged_decode_ref(q, kc, vc, bt_s, ctx, wl.num_heads, wl.num_kv_heads, wl.head_dim, wl.block_size,
-                         acc=np.float32)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+    q = wl.q[list(idx)].float().cpu().numpy()
+    return q, kc, vc, bt_s
+
+
+def cpu_baseline_decode(wl, seconds=10.0, sample_seqs=16, env=None):
+    """Time the oracle's float32 restatement of the reference's paged decode
+    (llama.py:97-144: padded gather to the table width, GQA expand, full scores,
+    -1e9 mask, softmax, PV) on the first ``sample_seqs`` sequences."""
+    from oracle.attention import paged_decode_ref
+    env = env or cpu_env()
+    idx = np.arange(min(sample_seqs, wl.batch))
+    q, kc, vc, bt_s = _compact_decode(wl, idx)
+    ctx = wl.context_lens[idx]
+    n, el = _time_cpu(lambda: paged_decode_ref(q, kc, vc, bt_s, ctx, wl.num_heads, wl.num_kv_heads, wl.head_dim,
+                                               wl.block_size, acc=np.float32), seconds)
     es = wl.k_cache.element_size()
     b = len(idx)
     blocks = int(((ctx.astype(np.int64) + wl.block_size - 1) // wl.block_size).sum())
     sample_bytes = (int(ctx.astype(np.int64).sum()) * wl.num_kv_heads * wl.head_dim * 2 * es
                     + b * wl.num_heads * wl.head_dim * 2 * es + blocks * 4 + b * 4)
-    threads = torch.get_num_threads()
-    return {
-        "value": round(sample_bytes * n / el / 1e9, 4),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"{b} of {wl.batch} sequences (sum ctx {int(ctx.sum())}), {n} passes in {el:.1f} s; "
-                   f"numpy float32 restatement of llama.py:97-144 incl. padded gather to the {bt.shape[1]}-block "
-                   f"table width; host cpus {len(os.sched_getaffinity(0))} of {os.cpu_count()}"),
-        "ms_per_call": round(el / n * 1e3, 3),
-    }
+    return _cpu_entry(round(sample_bytes * n / el / 1e9, 4), "GB/s",
+                      f"{b} of {wl.batch} sequences (sum ctx {int(ctx.sum())}), {n} passes in {el:.1f} s; numpy "
+                      f"float32 restatement of llama.py:97-144 incl. the padded gather to the {bt_s.shape[1]}-block "
+                      f"table width", env, ms_per_call=round(el / n * 1e3, 3), sample_bytes=sample_bytes)
 
+
+def cpu_baseline_prefill(wl, seconds=6.0, env=None):
+    """Time the oracle's float32 restatement of the reference's prefill attention
+    (llama.py:58-94: GQA expand, full L x L scores, -1e9 causal mask, softmax, PV)
+    on each prompt, and its per-chunk K/V write loop (llama.py:199-209 over
+    KVCache.write_kv, kv_cache.py:34-38)."""
+    from oracle.attention import flash_prefill_ref
+    from oracle.kv_cache import KVCacheRef
+    env = env or cpu_env()
+    per, flops_each = [], []
+    for i, length in enumerate(wl.lengths):
+        hq, hk, hv = wl.host[i]
+        n, el = _time_cpu(lambda: flash_prefill_ref(hq, hk, hv, True, acc=np.float32), seconds / 2 / len(wl.lengths))
+        per.append(el / n)
+        flops_each.append(4 * wl.num_heads * wl.head_dim * length * (length + 1) // 2)
+    cache = KVCacheRef(1, wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim, np.float16)
+    ks = [wl.host[i][1][0].astype(np.float16) for i in range(len(wl.lengths))]
+    vs = [wl.host[i][2][0].astype(np.float16) for i in range(len(wl.lengths))]
+    bs = wl.block_size
+
+    def write_loop():
+        for slots, k, v in zip(wl.slots, ks, vs):
+            pos, t = 0, len(slots)
+            while pos < t:                                   # llama.py:203-209
+                off = pos % bs
+                n = min(bs - off, t - pos)
+                cache.write_kv(0, int(slots[pos]) // bs, off, k[pos:pos + n], v[pos:pos + n])
+                pos += n
+
+    nw, elw = _time_cpu(write_loop, seconds / 2, min_iters=3)
+    tot = sum(per)
+    return _cpu_entry(round(sum(flops_each) / tot / 1e12, 5), "TFLOP/s",
+                      f"every prompt ({'+'.join(map(str, wl.lengths))} tokens), numpy float32 restatement of "
+                      f"llama.py:58-94 with the full L x L scores; K/V write loop of llama.py:199-209 "
+                      f"({sum(len(s) for s in wl.slots)} tokens, {nw} passes)", env,
+                      ms_per_prompt=[round(x * 1e3, 2) for x in per], kv_write_ms=round(elw / nw * 1e3, 3))
+
+
+def cpu_baseline_e2e(state, env=None):
+    """The oracle's float32 restatement of one batched decode step
+    (llama.py:290-388 over the reference layers; RMSNorm, interleaved RoPE,
+    paged attention with the padded gather, SwiGLU, greedy) at the workload's
+    batch, fed with the K/V the device wrote; one step timed, tok/s
+    extrapolated from it.  Its logits are the parity reference for the GPU's
+    step 1 (max-abs and the greedy match over the batch)."""
+    import torch
+    from oracle.llama import LlamaRef, greedy_ref
+    from tinyvllm_amd.llama import random_weights
+    env = env or cpu_env()
+    wl = state["wl"]
+    m, kv = wl.model, wl.kv
+    B, L = wl.batch, wl.prompt_len
+    t0 = time.perf_counter()
+    w = {name: t.float().cpu().numpy() for name, t in random_weights(m.config, seed=wl.seed).items()}
+    torch.cuda.empty_cache()
+    ref = LlamaRef(m.config, w, cache_dtype=np.float16)
+    ncols = L // kv.block_size + 1
+    ids = torch.from_numpy(wl.tables[:, :ncols].reshape(-1).astype(np.int64)).cuda()
+    kc = [k.index_select(0, ids).float().cpu().numpy() for k in kv.k_cache]
+    vc = [v.index_select(0, ids).float().cpu().numpy() for v in kv.v_cache]
+    tables = np.arange(B * ncols, dtype=np.int32).reshape(B, ncols)
+    prep = time.perf_counter() - t0
+    first = state["first"]
+    t0 = time.perf_counter()
+    want = ref.decode(first, [L] * B, [L + 1] * B, tables, kc, vc, kv.block_size)
+    el = time.perf_counter() - t0
+    got = state["step1_logits"]
+    return _cpu_entry(round(B / el, 3), "tok/s",
+                      f"one step at batch {B}, context {L} (the GPU's step 1, K/V gathered from the device), "
+                      f"numpy float32 restatement of llama.py:290-388; tok/s = {B} / step time "
+                      f"(the 128-step run extrapolated from one step)", env,
+                      ms_per_step=round(el * 1e3, 1), prep_s=round(prep, 1),
+                      parity={"step1_logits_max_abs": round(float(np.abs(got - want).max()), 6),
+                              "step1_greedy_match_rate": round(float(np.mean(np.argmax(got, 1) == greedy_ref(want))), 4),
+                              "tolerance": 2e-2, "sequences": B})
 
 def bench_decode(wl, steps, warmup, graph):
     from tinyvllm_amd.attention import PagedDecodePlan
@@ -159,7 +272,7 @@ def bench_prefill(steps, warmup):
     v8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
     ms8 = timed(PrefillPlan(q8, k8, v8, True).run, steps, warmup, graph=True)
     flops8 = 2 * hq8 * d8 * L8 * (L8 + 1)
-    return {
+    return wl, {
         "workload": "prefill_tinyllama_f16_L512+L1024 (Hq32 Hkv4 D64, causal) + fused KV write",
         "value": round(flops / (tot * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
         "ms_per_prompt": [round(x, 5) for x in per],
@@ -174,6 +287,19 @@ def bench_prefill(steps, warmup):
             "ms": round(ms8, 5), "flops": flops8,
             "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)},
     }
+
+
+def calibration_copy(mib):
+    """One plain device copy of ``mib`` MiB: the reference transfer the HBM
+    counters (FETCH_SIZE, WRITE_SIZE) are scaled by."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"bench: calibration copy of {n} bytes done")
 
 
 def bench_e2e(decode_steps=128, warmup=3):
@@ -213,7 +339,16 @@ def bench_e2e(decode_steps=128, warmup=3):
     ms = e0.elapsed_time(e1)
     hist = g.history[:, L + 1:L + 1 + decode_steps].cpu().numpy().astype(np.int64)
     nbytes = wl.bytes_for_steps(L, decode_steps)
-    return {
+    g.close()
+    # step 1 again from the prefilled state, keeping its logits for the parity
+    # check of the CPU leg (rows written by the timed steps past position L are
+    # never attended by step 1)
+    g1 = DecodeGraph(m, kv, B, wl.tables.shape[1])
+    g1.set_inputs(first, [L] * B, [L + 1] * B, wl.tables)
+    g1.step()
+    state = {"wl": wl, "first": first.cpu().numpy(), "step1_logits": g1.logits.cpu().numpy()}
+    g1.close()
+    return state, {
         "workload": "tinyllama_1.1b_random_init_f16 decode: B64, prompts 1024 (seeded), 128 greedy steps, "
                     "block16, shuffled pool +10%, one HIP graph per step",
         "value": round(B * decode_steps / (ms * 1e-3), 1), "unit": "tok/s",
@@ -222,6 +357,9 @@ def bench_e2e(decode_steps=128, warmup=3):
         "algorithmic_bytes": nbytes,
         "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic_per_step": STEP_TRAFFIC_BYTES,
+        "traffic_over_algorithmic": round(STEP_TRAFFIC_BYTES / wl.bytes_for_steps(L, 1), 4),
+        "traffic_source": STEP_TRAFFIC_SOURCE,
         "prefill_tok_s": round(B * L / (prefill_ms * 1e-3), 1),
         "prefill_ms": round(prefill_ms, 2),
         "tokens_checksum": int((hist * (np.arange(hist.size).reshape(hist.shape) % 9973 + 1)).sum()),
@@ -234,15 +372,20 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU time of the primary workload's baseline (the others take a few seconds each)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--primary-only", action="store_true")
     ap.add_argument("--e2e-only", action="store_true",
                     help="run only the end-to-end TinyLlama decode and print its result (profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the causal prefill + K/V write workload and print its result (profiling)")
+    ap.add_argument("--decode-long-only", action="store_true",
+                    help="run only the split-context decode B16 x 32768 and print its result (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (HBM counter calibration)")
+    ap.add_argument("--e2e-steps", type=int, default=128,
+                    help="decode steps of the end-to-end run with --e2e-only (profiling runs use fewer)")
     args = ap.parse_args()
     if args.gpus != 1:
         sys.exit("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -252,11 +395,18 @@ def main():
     from tinyvllm_amd import workloads
 
     torch.cuda.set_device(0)
-    if args.e2e_only:
-        print(json.dumps(bench_e2e()), flush=True)
-        return
-    if args.prefill_only:
-        print(json.dumps(bench_prefill(args.steps, args.warmup)), flush=True)
+    cpu_on = not args.no_cpu_baseline
+    env = cpu_env() if cpu_on else None
+    if args.e2e_only or args.prefill_only or args.decode_long_only:
+        if args.calib_copy_mib:
+            calibration_copy(args.calib_copy_mib)
+        if args.e2e_only:
+            out = bench_e2e(decode_steps=args.e2e_steps)[1]
+        elif args.prefill_only:
+            out = bench_prefill(args.steps, args.warmup)[1]
+        else:
+            out = config_decode_long(args, None, False)
+        print(json.dumps(out), flush=True)
         return
     log("bench: paged decode B256 Hq32 Hkv8 D128 fp16")
     wl3 = workloads.decode_llama3_8b_b256()
@@ -272,35 +422,35 @@ def main():
         configs["decode_tinyllama_f32_b4"] = {
             "value": round(r1["ms"] * 1e3, 3), "unit": "us", "gbs": round(r1["gbs"], 1),
             "bytes": r1["bytes"], "note": "cache-resident (~1 MB): latency-bound, not an HBM figure"}
+        if cpu_on:
+            cb = cpu_baseline_decode(wl1, seconds=3.0, sample_seqs=wl1.batch, env=env)
+            cb["us_per_call"] = round(cb["ms_per_call"] * 1e3, 1)
+            configs["decode_tinyllama_f32_b4"]["cpu_baseline"] = cb
         del wl1
         log("bench: causal prefill TinyLlama shape L512 + L1024 (and Llama-3-8B heads L2048)")
-        configs["prefill_tinyllama_f16"] = bench_prefill(args.steps, args.warmup)
+        wl2, configs["prefill_tinyllama_f16"] = bench_prefill(args.steps, args.warmup)
+        if cpu_on:
+            configs["prefill_tinyllama_f16"]["cpu_baseline"] = cpu_baseline_prefill(wl2, env=env)
+        del wl2
         log("bench: split-context decode B16 x 32768 bf16")
-        wl5 = workloads.decode_long_bf16_b16()
-        r5 = bench_decode(wl5, max(10, args.steps // 2), args.warmup, graph=False)
-        configs["decode_long_bf16_b16_32k"] = {
-            "value": round(r5["gbs"], 1), "unit": "GB/s", "ms": round(r5["ms"], 4),
-            "frac_of_hbm_peak": round(r5["gbs"] / HBM_PEAK_GBS, 4), "bytes": r5["bytes"],
-            "partition_size": r5["partition_size"]}
-        del wl5
+        configs["decode_long_bf16_b16_32k"] = config_decode_long(args, env, cpu_on)
+        torch.cuda.empty_cache()
         log("bench: TinyLlama-1.1B greedy decode B64, prompts 1024, 128 steps")
-        configs["e2e_tinyllama_decode"] = bench_e2e()
+        state, configs["e2e_tinyllama_decode"] = bench_e2e()
         log(f"bench: TinyLlama decode {configs['e2e_tinyllama_decode']['value']} tok/s")
+        if cpu_on:
+            log("bench: TinyLlama decode cpu baseline (one oracle step at B64)")
+            configs["e2e_tinyllama_decode"]["cpu_baseline"] = cpu_baseline_e2e(state, env=env)
+        del state
+        torch.cuda.empty_cache()
 
     if args.calib_copy_mib:
-        n = args.calib_copy_mib << 20
-        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"bench: calibration copy of {n} bytes done")
-        del src, dst
+        calibration_copy(args.calib_copy_mib)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if cpu_on:
         log("bench: cpu baseline (oracle float32 restatement)")
-        cpu = cpu_baseline_decode(wl3, seconds=args.cpu_seconds)
+        cpu = cpu_baseline_decode(wl3, seconds=args.cpu_seconds, env=env)
 
     line = {
         "metric": "paged-decode HBM GB/s (% of peak), prefill TFLOP/s, TinyLlama decode tok/s",
@@ -328,6 +478,22 @@ def main():
         "configs": configs,
     }
     print(json.dumps(line), flush=True)
+
+
+def config_decode_long(args, env, cpu_on):
+    """Split-context decode, Llama-3-8B heads, bf16, 16 sequences x 32768."""
+    from tinyvllm_amd import workloads
+    wl5 = workloads.decode_long_bf16_b16()
+    r5 = bench_decode(wl5, max(10, args.steps // 2), args.warmup, graph=False)
+    out = {"value": round(r5["gbs"], 1), "unit": "GB/s", "ms": round(r5["ms"], 4),
+           "frac_of_hbm_peak": round(r5["gbs"] / HBM_PEAK_GBS, 4), "bytes": r5["bytes"],
+           "partition_size": r5["partition_size"],
+           "traffic": LONG_TRAFFIC_BYTES, "traffic_over_algorithmic": round(LONG_TRAFFIC_BYTES / r5["bytes"], 4),
+           "traffic_source": LONG_TRAFFIC_SOURCE}
+    if cpu_on:
+        out["cpu_baseline"] = cpu_baseline_decode(wl5, seconds=4.0, sample_seqs=1, env=env)
+    del wl5
+    return out
 
 
 if __name__ == "__main__":
