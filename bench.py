@@ -272,6 +272,7 @@ def bench_prefill(steps, warmup):
     v8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
     ms8 = timed(PrefillPlan(q8, k8, v8, True).run, steps, warmup, graph=True)
     flops8 = 2 * hq8 * d8 * L8 * (L8 + 1)
+    chunk = bench_chunk_over_prefix(steps, warmup)
     return wl, {
         "workload": "prefill_tinyllama_f16_L512+L1024 (Hq32 Hkv4 D64, causal) + fused KV write",
         "value": round(flops / (tot * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
@@ -286,6 +287,7 @@ def bench_prefill(steps, warmup):
             "value": round(flops8 / (ms8 * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "ms": round(ms8, 5), "flops": flops8,
             "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)},
+        "chunk_over_cached_prefix": chunk,
     }
 
 
@@ -300,6 +302,49 @@ def calibration_copy(mib):
     dst.copy_(src)
     torch.cuda.synchronize()
     log(f"bench: calibration copy of {n} bytes done")
+
+
+def bench_chunk_over_prefix(steps, warmup, prefix=3584, chunk=512):
+    """A 512-token prompt chunk after a 3584-token cached prefix (TinyLlama heads,
+    fp16, block 16, shuffled blocks): the MFMA pass through the block table
+    (tv_flash_prefill_paged) against one paged decode query per chunk row over
+    the same table (the previous chunked-prefill path)."""
+    import ctypes
+    import math
+    import torch
+    from tinyvllm_amd import _lib
+    from tinyvllm_amd.attention import flash_prefill_paged
+    hq, hkv, d, bs = 32, 4, 64, 16
+    total = prefix + chunk
+    nblk = total // bs
+    rng = np.random.Generator(np.random.PCG64(3))
+    table = torch.from_numpy(rng.permutation(nblk + 8)[:nblk].astype(np.int32)).cuda()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    kc = torch.randn((nblk + 8, bs, hkv, d), generator=g, device="cuda").half()
+    vc = torch.randn((nblk + 8, bs, hkv, d), generator=g, device="cuda").half()
+    q = torch.randn((chunk, hq, d), generator=g, device="cuda").half()
+    ms_new = timed(lambda: flash_prefill_paged(q, kc, vc, table, prefix), steps, warmup, graph=False)
+    lib = _lib.load()
+    ctx = torch.arange(prefix + 1, total + 1, dtype=torch.int32, device="cuda")
+    out = torch.empty((chunk, 1, hq, d), dtype=torch.float16, device="cuda")
+    part = (total + 15) // 16 * 16
+    ws_bytes = lib.tv_paged_decode_workspace_bytes(chunk, hq, d, nblk, bs, part)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    args = (out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), table.data_ptr(), ctx.data_ptr(), chunk, hq,
+            hkv, d, bs, kc.shape[0], 0, nblk, 1.0 / math.sqrt(d), _lib.TV_F16, _lib.TV_F16, part,
+            ctypes.c_void_p(ws.data_ptr()), ws_bytes)
+
+    def per_row():
+        _lib.check(lib.tv_paged_decode(*args, _lib.stream_ptr(torch.device("cuda"))), "tv_paged_decode")
+    ms_old = timed(per_row, steps, warmup, graph=False)
+    new = flash_prefill_paged(q, kc, vc, table, prefix)[0]
+    per_row()
+    torch.cuda.synchronize()
+    flops = 4 * hq * d * (chunk * prefix + chunk * (chunk + 1) // 2)
+    return {"workload": f"chunk of {chunk} after {prefix} cached tokens, Hq32 Hkv4 D64 fp16, block 16 shuffled",
+            "value": round(flops / (ms_new * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms": round(ms_new, 5),
+            "per_row_decode_ms": round(ms_old, 5), "speedup": round(ms_old / ms_new, 2),
+            "max_abs_diff_vs_per_row": round(float((new.float() - out[:, 0].float()).abs().max()), 6)}
 
 
 def bench_e2e(decode_steps=128, warmup=3):

@@ -160,6 +160,26 @@ int tv_flash_prefill_varlen(void* out, const void* q, const void* k, const void*
                             int causal, float scale, int dtype, int out_dtype, void* stream);
 
 /*
+ * Prefill attention of one prompt chunk whose keys and values are read from the
+ * paged cache.  No counterpart in the reference, whose prefill at start_pos > 0
+ * attends within the chunk only (llama.py:184); chunked prefill over the cached
+ * prefix is on its roadmap (ROADMAP.md:75-99).  Query row i (q [q_len,
+ * num_heads, head_dim], token stride q_stride) sits at position start_pos + i
+ * and attends keys 0 .. start_pos + q_len - 1 of the sequence -- with causal,
+ * keys j <= start_pos + i -- where key j is row j % block_size of block
+ * block_table[j / block_size] of k_cache / v_cache [num_blocks, block_size,
+ * num_kv_heads, head_dim] (the chunk's own K/V must already be written).
+ * Equal to the last q_len rows of tv_flash_prefill over the whole sequence.
+ * fp16 / bf16, head_dim 64 or 128, block_size a power of two, at most 4096
+ * table entries (TV_EUNSUPPORTED otherwise).  A block id outside
+ * [0, num_blocks) makes the outputs of every head NaN (no out-of-bounds read).
+ */
+int tv_flash_prefill_paged(void* out, const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_table, int num_blocks, int block_size, int q_len, int start_pos,
+                           int num_heads, int num_kv_heads, int head_dim, int64_t q_stride, int64_t out_stride,
+                           int causal, float scale, int dtype, int out_dtype, void* stream);
+
+/*
  * Fused K/V cache write from a slot mapping.  Replaces the per-chunk
  * KVCache.write_kv loop (tinyvllm/core/kv_cache.py:34-38 called from
  * llama.py:199-209 and llama.py:381-386) with one launch:

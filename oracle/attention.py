@@ -140,11 +140,13 @@ def paged_decode_split_ref(queries, k_cache, v_cache, block_tables, context_lens
     return out
 
 
-def flash_prefill_ref(queries, keys, values, causal=True, acc=np.float64):
+def flash_prefill_ref(queries, keys, values, causal=True, acc=np.float64, q_offset=0):
     """Restates ``flash_prefill_attention`` (tinyvllm/model/llama.py:58-94).
 
     queries [1,Lq,Hq,D], keys [1,Lk,Hkv,D], values [1,Lk,Hkv,Dv] (batch must be
-    1, llama.py:65-67).  Returns [1,Lq,Hq,Dv] in ``acc``.
+    1, llama.py:65-67).  Returns [1,Lq,Hq,Dv] in ``acc``.  ``q_offset`` (no
+    reference counterpart; 0 is the reference) places query row i at position
+    i + q_offset for the causal mask: a chunk after a cached prefix.
     """
     q = np.asarray(queries)
     k = np.asarray(keys)
@@ -164,7 +166,7 @@ def flash_prefill_ref(queries, keys, values, causal=True, acc=np.float64):
     qt, kt, vt = q.transpose(1, 0, 2), k.transpose(1, 0, 2), v.transpose(1, 0, 2)
     scores = (qt @ kt.transpose(0, 2, 1)) * scale               # llama.py:84
     if causal:                                                  # llama.py:86-90
-        q_pos = np.arange(q_len).reshape(q_len, 1)
+        q_pos = np.arange(q_len).reshape(q_len, 1) + q_offset
         kv_pos = np.arange(kv_len).reshape(1, kv_len)
         scores = _masked_scores(scores, (kv_pos <= q_pos)[None])
     out = _softmax(scores) @ vt                                 # llama.py:92-93

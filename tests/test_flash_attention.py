@@ -337,3 +337,63 @@ def test_varlen_rejects_bad_arguments():
         flash_prefill_varlen(q, k, k, [10, 0])                 # empty prompt
     with pytest.raises(RuntimeError, match="head_dim 64 or 128"):
         flash_prefill_varlen(q.float(), k.float(), k.float(), [10])   # fp32: MFMA path only
+
+
+# ---- a chunk attending through the paged cache (no reference counterpart) -----------------
+
+def _paged_case(seed, total, hkv, d, bs, dtype, spare=5):
+    """A sequence of `total` tokens' K/V scattered over a shuffled block pool."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    nblk = -(-total // bs)
+    pool = nblk + spare
+    table = rng.permutation(pool)[:nblk].astype(np.int32)
+    k = randn(seed + 1, total, hkv, d, dtype=dtype)
+    v = randn(seed + 2, total, hkv, d, dtype=dtype)
+    kc = torch.zeros((pool, bs, hkv, d), dtype=dtype)
+    vc = torch.zeros_like(kc)
+    pos = np.arange(total)
+    kc.view(pool * bs, hkv, d)[torch.from_numpy(table[pos // bs] * bs + pos % bs).long()] = k
+    vc.view(pool * bs, hkv, d)[torch.from_numpy(table[pos // bs] * bs + pos % bs).long()] = v
+    return k, v, kc, vc, table
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d,hq,hkv", [(64, 32, 4), (128, 8, 2)])
+@pytest.mark.parametrize("start,n,bs,causal", [(0, 100, 16, True), (300, 77, 16, True), (1000, 256, 16, True),
+                                               (64, 64, 4, True), (200, 50, 32, False), (3584, 512, 16, True)])
+def test_paged_prefill_equals_last_rows_of_whole_prompt(dtype, d, hq, hkv, start, n, bs, causal):
+    """flash_prefill_paged: a chunk at start_pos reading K/V through a shuffled
+    block table equals the last n rows of prefill attention over the whole
+    sequence (the oracle on the contiguous rows; causal bottom-right aligned,
+    key j <= start + i), for block sizes 4, 16 and 32."""
+    from tinyvllm_amd.attention import flash_prefill_paged
+    total = start + n
+    k, v, kc, vc, table = _paged_case(200 + start + n, total, hkv, d, bs, dtype)
+    q = randn(97, total, hq, d, dtype=dtype)
+    out = flash_prefill_paged(q[start:].cuda(), kc.cuda(), vc.cuda(), torch.from_numpy(table).cuda(), start, causal)
+    torch.cuda.synchronize()
+    want = flash_prefill_ref(q[start:].float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None],
+                             causal, q_offset=start)[0]
+    assert np.abs(out[0].float().cpu().numpy() - want).max() <= TOL[dtype]
+
+
+def test_paged_prefill_invalid_block_id_gives_nan():
+    from tinyvllm_amd.attention import flash_prefill_paged
+    k, v, kc, vc, table = _paged_case(5, 80, 2, 64, 16, torch.float16)
+    table[2] = kc.shape[0] + 7
+    q = randn(98, 16, 8, 64, dtype=torch.float16)
+    out = flash_prefill_paged(q.cuda(), kc.cuda(), vc.cuda(), torch.from_numpy(table).cuda(), 64, True)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+
+
+def test_paged_prefill_rejects_bad_arguments():
+    from tinyvllm_amd.attention import flash_prefill_paged
+    kc = torch.zeros((4, 16, 2, 64), dtype=torch.float16, device="cuda")
+    q = torch.zeros((8, 4, 64), dtype=torch.float16, device="cuda")
+    table = torch.zeros(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError):
+        flash_prefill_paged(q, kc, kc, table, 30)                      # table covers 32 positions, needs 38
+    kc3 = torch.zeros((4, 12, 2, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="power of two"):
+        flash_prefill_paged(q, kc3, kc3, table, 0)

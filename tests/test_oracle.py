@@ -238,6 +238,22 @@ def test_prefill_top_left_alignment_for_unequal_lengths():
     assert np.abs(got[0, 0] - np.repeat(v[0, 0], 2, axis=0)).max() < 1e-12
 
 
+@pytest.mark.parametrize("start,n", [(0, 9), (5, 4), (12, 1), (3, 13)])
+def test_prefill_query_offset_equals_last_rows_of_whole_prompt(start, n):
+    """q_offset = s (a chunk after s cached positions) gives exactly the last n
+    rows of causal attention over the whole sequence (torch SDPA, float64) --
+    and differs from the top-left aligned chunk when s > 0 (the offset matters)."""
+    rng = _rng(14)
+    total = start + n
+    q = rng.standard_normal((1, total, 4, 8))
+    k = rng.standard_normal((1, total, 2, 8))
+    v = rng.standard_normal((1, total, 2, 8))
+    got = flash_prefill_ref(q[:, start:], k, v, True, q_offset=start)
+    assert np.abs(got - sdpa_prefill(q, k, v, True)[:, start:]).max() < 1e-12
+    if start > 0:
+        assert np.abs(got - flash_prefill_ref(q[:, start:], k, v, True)).max() > 1e-3
+
+
 def test_prefill_reference_known_answers():
     """test_flash_attention.py:123-139, restated."""
     rng = _rng(12)

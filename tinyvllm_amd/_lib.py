@@ -32,6 +32,7 @@ SIGNATURES = {
                               _I, _P, _S, _P]),
     "tv_flash_prefill_varlen": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _I, _I, _I, _L, _L, _L, _L,
                                      _I, _F, _I, _I, _P]),
+    "tv_flash_prefill_paged": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _L, _L, _I, _F, _I, _I, _P]),
     "tv_reshape_and_cache": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _L, _L, _I, _P, _P]),
     "tv_write_kv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _L, _L, _I, _P]),
     "tv_read_kv_blocks": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
@@ -51,7 +52,7 @@ SIGNATURES = {
     "tv_llama_prefill_workspace_bytes": (_S, [_P, _I]),
     "tv_llama_prefill": (_I, [_P, _P, _P, _P]),
 }
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 

@@ -140,6 +140,45 @@ def flash_prefill_attention(queries, keys, values, causal=True, *, out_dtype=Non
     return out
 
 
+def flash_prefill_paged(queries, k_cache, v_cache, block_table, start_pos, causal=True, *, out_dtype=None):
+    """Prefill of one prompt chunk whose keys and values come from the paged cache
+    (no counterpart in the reference: its chunk at start_pos > 0 attends within
+    the chunk only, llama.py:184; chunked prefill is on its roadmap,
+    ROADMAP.md:75-99).
+
+    queries [1, n, Hq, D] (or [n, Hq, D]) are the chunk's rows at positions
+    start_pos .. start_pos + n - 1; k_cache / v_cache [NB, bs, Hkv, D] already
+    hold the K/V of positions 0 .. start_pos + n - 1 at the blocks listed in
+    block_table (int32, one sequence, device).  Equals the last n rows of
+    ``flash_prefill_attention`` over the whole sequence.  fp16 / bf16, head_dim
+    64 or 128, power-of-two block size.  Returns [1, n, Hq, D].
+    """
+    lib = _lib.load()
+    dev = _on_gpu(queries, k_cache, v_cache, block_table)
+    q = queries[0] if queries.dim() == 4 else queries
+    _require(queries.dim() in (3, 4) and (queries.dim() == 3 or queries.shape[0] == 1),
+             "queries must be [1, n, Hq, D] or [n, Hq, D]")
+    _require(q.stride(2) == 1 and q.stride(1) == q.shape[2], "queries: heads and head_dim must be contiguous")
+    n, hq, d = q.shape
+    nb, bs, hkv, d2 = k_cache.shape
+    _require(tuple(v_cache.shape) == tuple(k_cache.shape) and d2 == d, "cache shape does not match the queries")
+    _require(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    _require(hq % hkv == 0, "query heads must be a multiple of KV heads")
+    _require(q.dtype == k_cache.dtype == v_cache.dtype, "queries and caches must share a dtype")
+    _require(block_table.dtype == torch.int32 and block_table.is_contiguous(), "block_table must be contiguous int32")
+    start_pos = int(start_pos)
+    _require(start_pos >= 0 and n > 0, "start_pos must be >= 0 and the chunk non-empty")
+    _require(block_table.numel() * bs >= start_pos + n, "block_table does not cover the sequence")
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    out = torch.empty((1, n, hq, d), dtype=out_dtype, device=dev)
+    rc = lib.tv_flash_prefill_paged(out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                    block_table.data_ptr(), nb, bs, n, start_pos, hq, hkv, d, q.stride(0), hq * d,
+                                    1 if causal else 0, 1.0 / math.sqrt(d), _lib.dtype_code(q.dtype),
+                                    _lib.dtype_code(out_dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "flash_prefill_paged")
+    return out
+
+
 class VarlenPrefillPlan:
     """Several prompts in one prefill launch (no reference counterpart: the
     engine prefills one sequence per call, engine.py:125-132).

@@ -46,7 +46,7 @@ constexpr int kPrefillBN = TV_PREFILL_BN;   // keys per unit of the chunking and
 
 // Key tiles query tile qt needs (causal rows stop at the diagonal).
 __device__ __forceinline__ int prefill_key_tiles(const PrefillParams& p, int qt) {
-  const int kend = p.causal ? min(p.kv_len, (qt + 1) * kPrefillBM) : p.kv_len;
+  const int kend = p.causal ? min(p.kv_len, (qt + 1) * kPrefillBM + p.q_pos_offset) : p.kv_len;
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
@@ -154,7 +154,11 @@ template <int KB> __device__ __forceinline__ float max_tile(const f32x4 (&st)[KB
 #define TV_PREFILL_WAVES_PER_EU 2
 #endif
 
-template <typename T, int D, int RB, int KS, int BN>
+// Block ids of a paged prompt staged in LDS per work-group (keys of up to
+// kPagedTableMax blocks: 65536 tokens at block size 16).
+constexpr int kPagedTableMax = 4096;
+
+template <typename T, int D, int RB, int KS, int BN, bool PAGED>
 __global__ void __launch_bounds__(256 / RB * KS) __attribute__((amdgpu_waves_per_eu(TV_PREFILL_WAVES_PER_EU)))
 prefill_fa_kernel(const PrefillParams pa) {
   // Several prompts per launch: this work-group's prompt is seq_order[blockIdx.z];
@@ -212,7 +216,8 @@ prefill_fa_kernel(const PrefillParams pa) {
   const int kt1 = min(kt0 + p.chunk_tiles, nkt);
   const int kbeg = kt0 * kPrefillBN;
   const int klim = min(kt1 * kPrefillBN, p.kv_len);                 // end before the causal limit
-  const int kend = p.causal ? min(klim, (qt + 1) * BM) : klim;
+  const int qoff = p.q_pos_offset;
+  const int kend = p.causal ? min(klim, (qt + 1) * BM + qoff) : klim;
   const int ntiles = (kend - kbeg + BN - 1) / BN;
   const float c = p.scale * kLog2e;
   const int row0 = qt * BM + wave * RB * 16;   // first query row of this wave
@@ -241,10 +246,35 @@ prefill_fa_kernel(const PrefillParams pa) {
   for (int i = 0; i < NV; ++i) {
     const int v = tid + i * GT;
     const int row = v / CPR, ch = v - (v / CPR) * CPR;
-    koff[i] = (int)(row * p.k_stride + ch * 8) * (int)sizeof(T);
-    voff[i] = (int)(row * p.v_stride + ch * 8) * (int)sizeof(T);
+    if constexpr (PAGED) {
+      koff[i] = row;            // row of the tile and element column: the cache row comes from the table
+      voff[i] = ch * 8;
+    } else {
+      koff[i] = (int)(row * p.k_stride + ch * 8) * (int)sizeof(T);
+      voff[i] = (int)(row * p.v_stride + ch * 8) * (int)sizeof(T);
+    }
     kdst[i] = row * KP + ch * 8;
     vdst[i] = SKT + row * VP + ch * 8;
+  }
+  // paged prompt: the block ids of keys [kbeg, kend) in LDS
+  __shared__ int stbl[PAGED ? kPagedTableMax : 1];
+  const int lg = p.kv_bs_log2;
+  const int blk0 = kbeg >> lg;
+  __shared__ int sbad;
+  bool bad = false;
+  const int kstage = max(kend, kbeg + 1);     // keys whose block ids are staged: [kbeg, kstage)
+  if constexpr (PAGED) {
+    const int nblk = ((kstage - 1) >> lg) - blk0 + 1;
+    if (threadIdx.x == 0) sbad = 0;
+    lds_barrier();
+    for (int i = threadIdx.x; i < nblk; i += blockDim.x) {
+      const int b = p.kv_table[blk0 + i];
+      const bool ok = (unsigned)b < (unsigned)p.kv_num_blocks;
+      stbl[i] = ok ? b : 0;                   // an invalid id reads block 0 (in bounds) ...
+      if (!ok) sbad = 1;
+    }
+    lds_barrier();
+    bad = sbad != 0;                          // ... and the head's outputs become NaN
   }
   struct Stage {
     u32x4 k[NV], v[NV];
@@ -261,13 +291,25 @@ prefill_fa_kernel(const PrefillParams pa) {
   const unsigned long long vbytes = ((unsigned long long)(p.kv_len - 1 - kbeg) * p.v_stride + D) * sizeof(T);
   auto gload = [&](int j, Stage& s) {
     const unsigned t = (unsigned)tile_of(j);
-    const unsigned long long ko = t * kstep, vo = t * vstep;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kfirst + ko, kbytes - ko);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vfirst + vo, vbytes - vo);
+    if constexpr (PAGED) {
+      // keys at or past kend (masked for every row of the unit) re-read the
+      // last staged key: the table is in LDS for keys [kbeg, kend) only
 #pragma unroll
-    for (int i = 0; i < NV; ++i) s.k[i] = buffer_load16(rk, koff[i], 0);
+      for (int i = 0; i < NV; ++i) {
+        const int key = max(kbeg, min(kbeg + (int)t * BN + koff[i], kstage - 1));
+        const long long row = ((long long)stbl[(key >> lg) - blk0] << lg) + (key & ((1 << lg) - 1));
+        s.k[i] = *reinterpret_cast<const u32x4*>(kbase + row * p.k_stride + voff[i]);
+        s.v[i] = *reinterpret_cast<const u32x4*>(vbase + row * p.v_stride + voff[i]);
+      }
+    } else {
+      const unsigned long long ko = t * kstep, vo = t * vstep;
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kfirst + ko, kbytes - ko);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vfirst + vo, vbytes - vo);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) s.v[i] = buffer_load16(rv, voff[i], 0);
+      for (int i = 0; i < NV; ++i) s.k[i] = buffer_load16(rk, koff[i], 0);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) s.v[i] = buffer_load16(rv, voff[i], 0);
+    }
   };
   auto lstore = [&](const Stage& s, int b) {
     uint16_t* t = tiles + b * BUF;
@@ -329,12 +371,12 @@ prefill_fa_kernel(const PrefillParams pa) {
         const u32x2 hi = lds_read_tr16(a + 16 * VP);
         vf[db][ks2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
-    if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0))) {
+    if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0 + qoff))) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         // last visible key, relative to this lane's first key k0 + 4 g: each
         // element is then one compare against a constant and one select
-        const int rel = (p.causal ? min(klim - 1, qi[r]) : klim - 1) - (k0 + 4 * g);
+        const int rel = (p.causal ? min(klim - 1, qi[r] + qoff) : klim - 1) - (k0 + 4 * g);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -464,7 +506,7 @@ prefill_fa_kernel(const PrefillParams pa) {
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
     if (qi[r] >= p.q_len) continue;
-    const float inv = 1.0f / lfin[r];
+    const float inv = bad ? __builtin_nanf("") : 1.0f / lfin[r];
     if (nchunks == 1) {
 #pragma unroll
       for (int db = 0; db < DB; ++db)
@@ -619,7 +661,7 @@ void prefill_units(const PrefillParams& p, int& units, int& max_chunks) {
   units = 0;
   max_chunks = 1;
   for (int qt = 0; qt < nqt; ++qt) {
-    const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM) : p.kv_len;
+    const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM + p.q_pos_offset) : p.kv_len;
     const int nkt = (kend + kPrefillBN - 1) / kPrefillBN;
     const int ch = (nkt + p.chunk_tiles - 1) / p.chunk_tiles;
     units += ch;
@@ -648,23 +690,24 @@ size_t prefill_workspace_bytes(const PrefillParams& p, int dtype) {
 
 // Key tiles of the last query tile (the longest causal row), host side.
 int prefill_key_tiles_host(const PrefillParams& p, int qt) {
-  const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM) : p.kv_len;
+  const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM + p.q_pos_offset) : p.kv_len;
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
 // Kernel shapes (16-row waves): 0 = 2 key groups (512 threads) of 64-key
 // tiles at head_dim 64, 32-key tiles at 128; 1 = 1 key group (256 threads) of
 // 64-key tiles at head_dim 64, 32-key at 128; 2 = 2 key groups of 32-key tiles.
-template <typename T, int D> void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
+template <typename T, int D, bool PAGED = false>
+void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
   constexpr int BN = D == 64 ? 64 : 32;
 #ifdef TV_PREFILL_FIXED
   (void)cfg;
-  hipLaunchKernelGGL((prefill_fa_kernel<T, D, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN>), grid,
+  hipLaunchKernelGGL((prefill_fa_kernel<T, D, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN, PAGED>), grid,
                      dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
 #else
-  if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, BN>), grid, dim3(512), 0, stream, pp);
-  else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, 32>), grid, dim3(512), 0, stream, pp);
-  else hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 1, BN>), grid, dim3(256), 0, stream, pp);
+  if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, BN, PAGED>), grid, dim3(512), 0, stream, pp);
+  else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, 32, PAGED>), grid, dim3(512), 0, stream, pp);
+  else hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 1, BN, PAGED>), grid, dim3(256), 0, stream, pp);
 #endif
 }
 
@@ -735,6 +778,35 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
   if (dtype == kF32) hipLaunchKernelGGL((prefill_generic_kernel<float>), grid, dim3(64), 0, stream, p_in);
   else if (dtype == kF16) hipLaunchKernelGGL((prefill_generic_kernel<_Float16>), grid, dim3(64), 0, stream, p_in);
   else hipLaunchKernelGGL((prefill_generic_kernel<__bf16>), grid, dim3(64), 0, stream, p_in);
+  return 0;
+}
+
+// One prompt whose keys and values are read through a block table
+// (kv_table set) with query rows at positions q_pos_offset ..: the 64-row
+// kernel with its loads going through the table.  Returns 1 when the shape has
+// no such kernel (fp32, head_dim other than 64 / 128, a block size that is
+// not a power of two, or more than kPagedTableMax blocks).
+int launch_flash_prefill_paged(const PrefillParams& p_in, int dtype, hipStream_t stream) {
+  PrefillParams pp = p_in;
+  if (!prefill_uses_mfma(pp, dtype) || !pp.kv_table || pp.kv_bs_log2 < 0 || pp.kv_bs_log2 > 20) return 1;
+  if (((long long)pp.kv_len + (1LL << pp.kv_bs_log2) - 1) >> pp.kv_bs_log2 > kPagedTableMax) return 1;
+  pp.xcd_remap = (pp.num_heads % 8 == 0) ? 1 : 0;
+  pp.chunk_tiles = 1 << 20;
+  int units, max_chunks;
+  prefill_units(pp, units, max_chunks);
+  pp.max_chunks = 1;
+  const bool d64 = pp.head_dim == 64;
+  const dim3 grid(pp.num_heads, units);
+  const long long wgs = (long long)grid.x * grid.y;
+  const bool long_rows = prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8;
+  const int cfg = long_rows && wgs <= 256 ? 0 : (d64 && long_rows && wgs < 1024 ? 2 : 1);
+  if (dtype == kF16) {
+    if (d64) launch_fa<_Float16, 64, true>(cfg, grid, pp, stream);
+    else launch_fa<_Float16, 128, true>(cfg, grid, pp, stream);
+  } else {
+    if (d64) launch_fa<__bf16, 64, true>(cfg, grid, pp, stream);
+    else launch_fa<__bf16, 128, true>(cfg, grid, pp, stream);
+  }
   return 0;
 }
 

@@ -261,13 +261,20 @@ int attend_unfused(const tv_llama_model* m, const tv_llama_cache* c, const Layer
     }
   } else if (io.pargs->attend_prefix && io.pargs->start_pos > 0) {
     // chunked prefill over the cached prefix: the chunk's k/v are in the cache
-    // now, so row i is a paged decode of context start_pos + i + 1 over the
-    // sequence's one table row (stride 0), whole context per work-group
+    // now, so the chunk attends keys 0 .. start_pos + M - 1 through the
+    // sequence's table (MFMA tiles, causal at offset start_pos)
     const tv_llama_prefill_args* a = io.pargs;
-    const int width = a->bt_width * c->block_size;
-    rc = tv_paged_decode(io.attn, io.q, c->k_caches[l], c->v_caches[l], a->block_table, io.slots, M, m->n_heads,
-                         m->n_kv_heads, m->head_dim, c->block_size, c->num_blocks, 0, a->bt_width, scale, dt, dt,
-                         (width + 15) / 16 * 16, io.attn_ws, io.attn_ws_bytes, s);
+    rc = tv_flash_prefill_paged(io.attn, io.q, c->k_caches[l], c->v_caches[l], a->block_table, c->num_blocks,
+                                c->block_size, M, a->start_pos, m->n_heads, m->n_kv_heads, m->head_dim, qd, qd, 1,
+                                scale, dt, dt, s);
+    if (rc == TV_EUNSUPPORTED) {
+      // fp32 models, odd head sizes or block sizes: row i is a paged decode of
+      // context start_pos + i + 1 over the sequence's one table row (stride 0)
+      const int width = a->bt_width * c->block_size;
+      rc = tv_paged_decode(io.attn, io.q, c->k_caches[l], c->v_caches[l], a->block_table, io.slots, M, m->n_heads,
+                           m->n_kv_heads, m->head_dim, c->block_size, c->num_blocks, 0, a->bt_width, scale, dt, dt,
+                           (width + 15) / 16 * 16, io.attn_ws, io.attn_ws_bytes, s);
+    }
     if (rc != TV_OK) return rc;
   } else {
     rc = tv_flash_prefill(io.attn, io.q, io.kst, io.vst, M, M, m->n_heads, m->n_kv_heads, m->head_dim,

@@ -120,7 +120,7 @@ int decode_scratch(void** ptr) {
 
 extern "C" {
 
-int tv_abi_version(void) { return 7; }
+int tv_abi_version(void) { return 8; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
@@ -413,6 +413,40 @@ int tv_flash_prefill_varlen(void* out, const void* q, const void* k, const void*
                 "tv_flash_prefill_varlen: fp16 / bf16, head_dim 64 or 128 and 16-byte aligned rows only "
                 "(dtype %d, head_dim %d)", dtype, head_dim);
   return check_launch("tv_flash_prefill_varlen");
+}
+
+int tv_flash_prefill_paged(void* out, const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_table, int num_blocks, int block_size, int q_len, int start_pos,
+                           int num_heads, int num_kv_heads, int head_dim, int64_t q_stride, int64_t out_stride,
+                           int causal, float scale, int dtype, int out_dtype, void* stream) {
+  if (!out || !q || !k_cache || !v_cache || !block_table)
+    return fail(TV_EINVAL, "tv_flash_prefill_paged: null pointer argument");
+  if (!valid_dtype(dtype) || !(out_dtype == dtype || out_dtype == TV_F32))
+    return fail(TV_EINVAL, "tv_flash_prefill_paged: bad dtype %d / out_dtype %d", dtype, out_dtype);
+  if (q_len <= 0 || start_pos < 0 || num_blocks <= 0 || block_size <= 0 || (long long)start_pos + q_len > (1LL << 30))
+    return fail(TV_EINVAL, "tv_flash_prefill_paged: bad sizes (q_len=%d, start_pos=%d, num_blocks=%d, block_size=%d)",
+                q_len, start_pos, num_blocks, block_size);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads > 65535)
+    return fail(TV_EINVAL, "tv_flash_prefill_paged: bad head counts (%d, %d)", num_heads, num_kv_heads);
+  if (q_stride < (int64_t)num_heads * head_dim || out_stride < (int64_t)num_heads * head_dim)
+    return fail(TV_EINVAL, "tv_flash_prefill_paged: token stride smaller than a token row");
+  if (!pow2(block_size)) return fail(TV_EUNSUPPORTED, "tv_flash_prefill_paged: block_size %d is not a power of two",
+                                     block_size);
+  if (q_len > 65535 * 64) return fail(TV_EINVAL, "tv_flash_prefill_paged: grid too large");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  tv::PrefillParams p;
+  prefill_params(p, out, q, k_cache, v_cache, q_len, start_pos + q_len, num_heads, num_kv_heads, head_dim, head_dim,
+                 q_stride, row, row, out_stride, causal, scale, out_dtype, 0);
+  p.kv_table = block_table;
+  p.kv_bs_log2 = ilog2(block_size);
+  p.kv_num_blocks = num_blocks;
+  p.q_pos_offset = start_pos;
+  const int rc = tv::launch_flash_prefill_paged(p, dtype, reinterpret_cast<hipStream_t>(stream));
+  if (rc == 1)
+    return fail(TV_EUNSUPPORTED,
+                "tv_flash_prefill_paged: fp16 / bf16, head_dim 64 or 128, 16-byte aligned rows and at most 4096 "
+                "blocks only (dtype %d, head_dim %d)", dtype, head_dim);
+  return check_launch("tv_flash_prefill_paged");
 }
 
 static int kv_write_common(const char* name, void* k_cache, void* v_cache, const void* k, const void* v,

@@ -35,6 +35,17 @@ struct PrefillParams {
   const int* cu_q;
   const int* cu_k;
   const int* seq_order;
+  // Keys and values in a paged cache (null: k / v are contiguous rows).  Key
+  // j of the prompt is cache row kv_table[j >> kv_bs_log2] * 2^kv_bs_log2 +
+  // (j & (2^kv_bs_log2 - 1)); k / v point at the cache base, k_stride /
+  // v_stride are the cache row strides (num_kv_heads * head_dim).
+  const int* kv_table;
+  int kv_bs_log2;
+  int kv_num_blocks;     // ids outside [0, kv_num_blocks) make the head's outputs NaN
+  // Absolute position of query row 0: causal rows see keys j <= i + q_pos_offset
+  // (0: top-left aligned, the reference's prompt; start_pos: a chunk after a
+  // cached prefix).
+  int q_pos_offset;
 };
 
 // Cache write from a slot mapping or a base slot (kv_cache.hip).
@@ -71,6 +82,7 @@ size_t prefill_workspace_bytes(const PrefillParams& p, int dtype);
 int launch_flash_prefill(const PrefillParams& p, int dtype, void* workspace, size_t workspace_bytes,
                          hipStream_t stream);
 bool launch_prefill_rows(const PrefillParams& p, int dtype, int num_seqs, int max_q_len, hipStream_t stream);
+int launch_flash_prefill_paged(const PrefillParams& p, int dtype, hipStream_t stream);
 int launch_flash_prefill_varlen(const PrefillParams& p, int num_seqs, int max_q_len, int max_kv_len,
                                 long long total_q, int dtype, hipStream_t stream);
 void launch_kv_write(const KVWriteParams& p, int vec_bytes, hipStream_t stream);
