@@ -21,7 +21,9 @@ bounded sample -- the padded-gather decode (llama.py:97-144), the full L x L
 prefill and per-chunk K/V write loop (llama.py:58-94, 199-209), and one batched
 decode step of the model (llama.py:290-388), whose logits also check the GPU's
 step 1.  ``traffic`` figures come from rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-recorded under profiles/.
+recorded under profiles/.  ``hbm_read_ceiling`` is the part's measured
+streaming-read rate (tv_stream_read over 2 GiB), which the HBM-bound decode
+figures are also quoted against (``frac_of_read_ceiling``).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -304,6 +306,45 @@ def calibration_copy(mib):
     log(f"bench: calibration copy of {n} bytes done")
 
 
+def bench_read_ceiling(steps=20, warmup=5, gib=2):
+    """The part's streaming-read ceiling: tv_stream_read over a 2 GiB buffer (8x
+    the 256 MB memory-side cache), ordinary and non-temporal 16-byte loads, 4 or
+    8 in flight per lane, 2-16 work-groups of 256 lanes per CU, each reading
+    one contiguous range or strided over the whole grid.  The HBM-bound
+    kernels are quoted against the 8 TB/s peak and against this ceiling."""
+    import ctypes
+    import torch
+    from tinyvllm_amd import _lib
+    lib = _lib.load()
+    n = gib << 30
+    buf = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(3)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(16 * cus, dtype=torch.int32, device="cuda")      # one word per work-group
+    variants = {}
+    for contig in (0, 1):
+        for nt in (0, 1):
+            for u in (4, 8):
+                for per_cu in (2, 4, 8, 16):
+                    wg = per_cu * cus
+
+                    def fn(nt=nt, u=u, wg=wg, contig=contig):
+                        rc = lib.tv_stream_read(ctypes.c_void_p(buf.data_ptr()), n, nt, u, wg, contig,
+                                                ctypes.c_void_p(sink.data_ptr()),
+                                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                        if rc != 0:
+                            raise RuntimeError(lib.tv_last_error().decode())
+                    ms = timed(fn, steps, warmup)
+                    name = f"{'contig' if contig else 'strided'}_{'nt' if nt else 'plain'}_u{u}_wg{per_cu}x"
+                    variants[name] = round(n / (ms * 1e-3) / 1e9, 1)
+    best = max(variants, key=variants.get)
+    del buf
+    return {"value": variants[best], "unit": "GB/s", "frac_of_hbm_peak": round(variants[best] / HBM_PEAK_GBS, 4),
+            "best": best, "bytes": n, "best_plain": max(v for k, v in variants.items() if "_plain_" in k),
+            "variants": variants,
+            "note": "read-only stream of 16-byte vectors; variant = layout (one contiguous range per "
+                    "work-group or strided over the grid), load kind, loads in flight per lane, work-groups per CU"}
+
+
 def bench_chunk_over_prefix(steps, warmup, prefix=3584, chunk=512):
     """A 512-token prompt chunk after a 3584-token cached prefix (TinyLlama heads,
     fp16, block 16, shuffled blocks): the MFMA pass through the block table
@@ -429,6 +470,8 @@ def main():
                     help="run only the split-context decode B16 x 32768 and print its result (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (HBM counter calibration)")
+    ap.add_argument("--read-ceiling-only", action="store_true",
+                    help="run only the streaming-read ceiling and print its result (profiling)")
     ap.add_argument("--e2e-steps", type=int, default=128,
                     help="decode steps of the end-to-end run with --e2e-only (profiling runs use fewer)")
     args = ap.parse_args()
@@ -442,10 +485,12 @@ def main():
     torch.cuda.set_device(0)
     cpu_on = not args.no_cpu_baseline
     env = cpu_env() if cpu_on else None
-    if args.e2e_only or args.prefill_only or args.decode_long_only:
+    if args.e2e_only or args.prefill_only or args.decode_long_only or args.read_ceiling_only:
         if args.calib_copy_mib:
             calibration_copy(args.calib_copy_mib)
-        if args.e2e_only:
+        if args.read_ceiling_only:
+            out = bench_read_ceiling()
+        elif args.e2e_only:
             out = bench_e2e(decode_steps=args.e2e_steps)[1]
         elif args.prefill_only:
             out = bench_prefill(args.steps, args.warmup)[1]
@@ -488,6 +533,12 @@ def main():
             configs["e2e_tinyllama_decode"]["cpu_baseline"] = cpu_baseline_e2e(state, env=env)
         del state
         torch.cuda.empty_cache()
+        log("bench: streaming-read ceiling (2 GiB)")
+        ceiling = bench_read_ceiling()
+        configs["hbm_read_ceiling"] = ceiling
+        for key in ("decode_long_bf16_b16_32k",):
+            configs[key]["frac_of_read_ceiling"] = round(configs[key]["value"] / ceiling["value"], 4)
+        torch.cuda.empty_cache()
 
     if args.calib_copy_mib:
         calibration_copy(args.calib_copy_mib)
@@ -519,6 +570,8 @@ def main():
                      "traffic_source": PRIMARY_TRAFFIC_SOURCE,
                      "algorithmic_bytes_per_launch": r3["bytes"],
                      "timing": "HIP events over K launches of decode+merge on the launch stream"},
+        "frac_of_read_ceiling": (round(r3["gbs"] / configs["hbm_read_ceiling"]["value"], 4)
+                                 if "hbm_read_ceiling" in configs else None),
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -14,7 +14,7 @@ LIB_PATH = Path(os.environ.get("TV_ATTN_LIB", _PKG / "libtvattn.so"))
 TV_F32, TV_F16, TV_BF16 = 0, 1, 2
 TV_OK, TV_EINVAL, TV_EUNSUPPORTED, TV_EHIP = 0, 1, 2, 3
 
-# name -> (restype, argtypes); mirrors include/tv_attn.h
+# name -> (restype, argtypes); mirrors include/tv_attn.h, tv_llama.h and tv_bench.h
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
@@ -51,8 +51,10 @@ SIGNATURES = {
     "tv_llama_graph_destroy": (_I, [_P]),
     "tv_llama_prefill_workspace_bytes": (_S, [_P, _I]),
     "tv_llama_prefill": (_I, [_P, _P, _P, _P]),
+    # include/tv_bench.h
+    "tv_stream_read": (_I, [_P, _L, _I, _I, _I, _I, _P, _P]),
 }
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 

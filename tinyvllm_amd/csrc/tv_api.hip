@@ -120,7 +120,7 @@ int decode_scratch(void** ptr) {
 
 extern "C" {
 
-int tv_abi_version(void) { return 8; }
+int tv_abi_version(void) { return 9; }
 
 const char* tv_last_error(void) { return tv::last_error(); }
 
