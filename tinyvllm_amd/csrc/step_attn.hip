@@ -22,6 +22,16 @@
 
 namespace tv {
 
+// 16 bytes of a cached K / V row: ordinary or non-temporal load.  V rows are
+// read whole (8 lanes per 128-byte row) and stream non-temporally; a K load
+// instruction reads half of each 128-byte row (the MFMA operand layout), and
+// non-temporal K loads made the TinyLlama decode step 4% slower (V alone: 0.2%
+// faster).
+template <int NT, typename E> __device__ __forceinline__ u32x4 ld_tile(const E* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else return *reinterpret_cast<const u32x4*>(p);
+}
+
 template <typename T, int D, int NW, int PF>
 __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams p) {
   constexpr int KS = D / 32;        // MFMA k steps over the head dim
@@ -92,8 +102,8 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
     // K rows: lane (token col of the half, 8-dim group g)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      r.k[0][ks] = *reinterpret_cast<const u32x4*>(kcache + base0 + col * rs + 32 * ks + 8 * g);
-      r.k[1][ks] = *reinterpret_cast<const u32x4*>(kcache + base1 + col * rs + 32 * ks + 8 * g);
+      r.k[0][ks] = ld_tile<0>(kcache + base0 + col * rs + 32 * ks + 8 * g);
+      r.k[1][ks] = ld_tile<0>(kcache + base1 + col * rs + 32 * ks + 8 * g);
     }
     // V rows: unit (token, 16-byte chunk), staged row-major in LDS
 #pragma unroll
@@ -101,7 +111,7 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
       const int unit = lane + 64 * i;
       const int tok = unit / CPR;
       const int ch = unit % CPR;
-      r.v[i] = *reinterpret_cast<const u32x4*>(vcache + (tok < 16 ? base0 : base1) + (size_t)(tok & 15) * rs + 8 * ch);
+      r.v[i] = ld_tile<1>(vcache + (tok < 16 ? base0 : base1) + (size_t)(tok & 15) * rs + 8 * ch);
     }
   };
 
