@@ -171,8 +171,10 @@ int tv_flash_prefill_varlen(void* out, const void* q, const void* k, const void*
  * num_kv_heads, head_dim] (the chunk's own K/V must already be written).
  * Equal to the last q_len rows of tv_flash_prefill over the whole sequence.
  * fp16 / bf16, head_dim 64 or 128, block_size a power of two, at most 4096
- * table entries (TV_EUNSUPPORTED otherwise).  A block id outside
- * [0, num_blocks) makes the outputs of every head NaN (no out-of-bounds read).
+ * table entries (TV_EUNSUPPORTED otherwise).  block_table holds at least
+ * ceil((start_pos + q_len) / block_size) entries.  A block id outside
+ * [0, num_blocks) is never dereferenced: the rows of every 64-row query tile
+ * whose keys include that block come out NaN in every head.
  */
 int tv_flash_prefill_paged(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int num_blocks, int block_size, int q_len, int start_pos,
