@@ -18,7 +18,7 @@ Follows tinyvllm/model/llama.py step by step:
 * ``round_bf16``        storage rounding of a bfloat16 cache (no reference counterpart:
                         the reference has no bfloat16, weights.py:44)
 
-Arithmetic is float32 (the north-star reference precision); the paged cache stores
+Arithmetic is float32 (the precision the fp16 / bf16 kernels are held to); the paged cache stores
 ``cache_dtype`` (float16 by default, as KVCache(dtype=float16), kv_cache.py:25-32).
 Weights use the reference's Meta-style names (``layers.{i}.attention.wq.weight``, ...,
 llama.py:413-416).

@@ -142,7 +142,7 @@ def test_dense_entry_points_validate_on_host():
 
 
 def test_decode_step_workspace_tinyllama():
-    """Workspace of the TinyLlama-1.1B step at batch 64 (the config-4 shape)."""
+    """Workspace of the TinyLlama-1.1B step at batch 64 (the end-to-end decode workload)."""
     from tinyvllm_amd.llama import LlamaConfig, _Model
     c = LlamaConfig.tinyllama_1b()
     m = _Model(c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim, c.hidden_dim, c.vocab_size, _lib.TV_F16,
