@@ -39,6 +39,13 @@
 // over two 4-wave groups in ping-pong (one group's MFMA phase against the
 // other's softmax phase, a barrier per phase) was correct but 2x slower: the
 // softmax phase of one wave ran ~4x longer while the other issued MFMAs.
+// Balancing the causal work by pairing query tiles i and nqt-1-i was correct
+// but no faster at L 2048: split over the two 4-wave groups of one 8-wave
+// work-group (both waves of a SIMD then pass the same barrier, in phase) or
+// run back to back by one work-group (one work-group per CU leaves one wave
+// per SIMD, ~1.1 us per tile step against ~1.5 us for two waves' steps
+// together).  Two independent work-groups per CU, drifting out of phase, are
+// what keeps the matrix pipes busiest here.
 #include "tv_common.h"
 #include "tv_params.h"
 
