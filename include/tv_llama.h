@@ -167,8 +167,8 @@ typedef struct tv_llama_prefill_args {
   int num_tokens;
   const int32_t* tokens;        /* [num_tokens] */
   int start_pos;
-  const int32_t* block_table;   /* this sequence's table row */
-  int bt_width;
+  const int32_t* block_table;   /* this sequence's table row: bt_width entries covering */
+  int bt_width;                 /* positions 0 .. start_pos + num_tokens - 1 (TV_EINVAL otherwise) */
   float* logits;                /* [num_tokens, vocab], or [1, vocab] with logits_last_only, or NULL */
   int logits_last_only;
   int32_t* next_token;          /* [1] greedy token after the last position, or NULL */

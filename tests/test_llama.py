@@ -668,3 +668,29 @@ def test_load_weights_sets_found_names_and_keeps_the_rest():
             assert torch.equal(a, b)
     with pytest.raises(ValueError):
         want.load_weights({"output.weight": torch.zeros(3, 3)})
+
+
+def test_prefill_abi_rejects_a_table_short_of_the_prompt():
+    """tv_llama_prefill checks, before any launch, that the block table covers
+    positions 0 .. start_pos + n - 1 (Llama.prefill_table checks it in Python;
+    a raw C caller gets TV_EINVAL instead of a read past the table)."""
+    import ctypes
+    from tinyvllm_amd import _lib
+    from tinyvllm_amd.llama import _PrefillArgs
+    cfg = small_config()
+    model, kv, *_ = build(cfg, seed=8)
+    lib = _lib.load()
+    n = 20
+    toks = torch.zeros(n, dtype=torch.int32, device="cuda")
+    table = torch.zeros(1, dtype=torch.int32, device="cuda")       # one block of 16 positions
+    need = lib.tv_llama_prefill_workspace_bytes(ctypes.byref(model._model), n)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    cache, keep = model.cache_struct(kv)
+    for start, attend in ((0, 0), (10, 1)):
+        args = _PrefillArgs(n, toks.data_ptr(), start, table.data_ptr(), table.numel(), None, 0, None,
+                            ws.data_ptr(), ws.numel(), attend)
+        rc = lib.tv_llama_prefill(ctypes.byref(model._model), ctypes.byref(cache), ctypes.byref(args),
+                                  _lib.stream_ptr(model.device))
+        assert rc == _lib.TV_EINVAL
+        assert b"block table covers 16 positions" in lib.tv_last_error()
+    del keep

@@ -562,6 +562,9 @@ int tv_llama_prefill(const tv_llama_model* m, const tv_llama_cache* c, const tv_
     return fail(TV_EINVAL, "tv_llama_prefill: bad prefill arguments");
   if (a->logits && !aligned16(a->logits)) return fail(TV_EINVAL, "tv_llama_prefill: logits must be 16-byte aligned");
   const int M = a->num_tokens;
+  if ((long long)a->start_pos + M > (long long)a->bt_width * c->block_size)
+    return fail(TV_EINVAL, "tv_llama_prefill: the block table covers %lld positions, the chunk ends at %lld",
+                (long long)a->bt_width * c->block_size, (long long)a->start_pos + M);
   const StepLayout L = step_layout(m, M, 1, 1, 1, false);
   if (!a->workspace || a->workspace_bytes < L.total || !aligned16(a->workspace))
     return fail(TV_EINVAL, "tv_llama_prefill: workspace of %zu bytes required (got %zu)", L.total, a->workspace_bytes);
