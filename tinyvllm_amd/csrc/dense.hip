@@ -300,37 +300,56 @@ void launch_linear(const LinearParams& p, int epi, int dtype, hipStream_t s) {
 // or residual, split partials) is issued before the first add, one LDS
 // reduction gives the mean square, and the normalised row is written from
 // registers.
-template <typename T, int VPT>
+// MODE: kNormEmb (x = emb[tokens]), kNormPart (x += the split partials) or
+// kNormPlain (x as it is).  One instantiation per mode keeps every load of the
+// row in one basic block, so the weight, residual and first batch of partials
+// are all requested before the first wait.
+enum NormMode : int { kNormEmb = 0, kNormPart = 1, kNormPlain = 2 };
+
+template <typename T, int VPT, int MODE>
 __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
   __shared__ float red[4];
   const int m = blockIdx.x;
   float* x = p.x + (size_t)m * p.dim;
+  // SB splits per batch of loads: all of a product's splits in one round trip
+  // at the decode step's sizes; indexes past the last split re-read it and are
+  // dropped
+  constexpr int SB = VPT <= 2 ? 8 : 4;
+  f32x4 v[VPT], w[VPT], t[MODE == kNormPart ? SB : 1][VPT];
   int tok = 0;
-  if (p.emb) tok = min(max(p.tokens[m], 0), p.vocab - 1);
-  f32x4 v[VPT], w[VPT];
+  if constexpr (MODE == kNormEmb) tok = min(max(p.tokens[m], 0), p.vocab - 1);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int k = min(4 * (threadIdx.x + 256 * i), p.dim - 4);   // clamped: lanes past dim re-read the last vector
     w[i] = *reinterpret_cast<const f32x4*>(p.weight + k);
-    if (p.emb) {
+    if constexpr (MODE == kNormEmb) {
       v[i] = load4<T>(p.emb, (size_t)tok * p.dim + k);
     } else {
       v[i] = *reinterpret_cast<const f32x4*>(x + k);
     }
-  }
-  if (p.part) {
-    // four splits per batch of loads; indexes past the last split re-read it and are dropped
-    for (int s0 = 0; s0 < p.splits; s0 += 4) {
-      f32x4 t[4][VPT];
+    if constexpr (MODE == kNormPart) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < SB; ++u)
+        t[u][i] = *reinterpret_cast<const f32x4*>(p.part + ((size_t)min(u, p.splits - 1) * p.M + m) * p.dim + k);
+    }
+  }
+  if constexpr (MODE == kNormPart) {
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+      if (u < p.splits) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) v[i] += t[u][i];
+      }
+    for (int s0 = SB; s0 < p.splits; s0 += SB) {
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
           const int k = min(4 * (threadIdx.x + 256 * i), p.dim - 4);
           t[u][i] = *reinterpret_cast<const f32x4*>(p.part + ((size_t)min(s0 + u, p.splits - 1) * p.M + m) * p.dim + k);
         }
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < SB; ++u)
         if (s0 + u < p.splits) {
 #pragma unroll
           for (int i = 0; i < VPT; ++i) v[i] += t[u][i];
@@ -342,7 +361,7 @@ __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
   for (int i = 0; i < VPT; ++i) {
     const int k = 4 * (threadIdx.x + 256 * i);
     if (k < p.dim) {
-      if (p.emb || p.part) *reinterpret_cast<f32x4*>(x + k) = v[i];
+      if constexpr (MODE != kNormPlain) *reinterpret_cast<f32x4*>(x + k) = v[i];
       ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
     }
   }
@@ -359,12 +378,18 @@ __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
   }
 }
 
+template <typename T, int VPT> void launch_norm_v(const NormParams& p, hipStream_t s) {
+  if (p.emb) hipLaunchKernelGGL((norm_kernel<T, VPT, kNormEmb>), dim3(p.M), dim3(256), 0, s, p);
+  else if (p.part) hipLaunchKernelGGL((norm_kernel<T, VPT, kNormPart>), dim3(p.M), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((norm_kernel<T, VPT, kNormPlain>), dim3(p.M), dim3(256), 0, s, p);
+}
+
 template <typename T> void launch_norm_t(const NormParams& p, hipStream_t s) {
   const int vpt = (p.dim + 1023) / 1024;
-  if (vpt <= 1) hipLaunchKernelGGL((norm_kernel<T, 1>), dim3(p.M), dim3(256), 0, s, p);
-  else if (vpt <= 2) hipLaunchKernelGGL((norm_kernel<T, 2>), dim3(p.M), dim3(256), 0, s, p);
-  else if (vpt <= 4) hipLaunchKernelGGL((norm_kernel<T, 4>), dim3(p.M), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((norm_kernel<T, 8>), dim3(p.M), dim3(256), 0, s, p);
+  if (vpt <= 1) launch_norm_v<T, 1>(p, s);
+  else if (vpt <= 2) launch_norm_v<T, 2>(p, s);
+  else if (vpt <= 4) launch_norm_v<T, 4>(p, s);
+  else launch_norm_v<T, 8>(p, s);
 }
 
 void launch_norm(const NormParams& p, int dtype, hipStream_t s) {

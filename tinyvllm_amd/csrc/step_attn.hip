@@ -115,44 +115,58 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
     }
   };
 
+  // ---- q, k, v of the new token: loads ------------------------------------
+  // Thread tid's first item of the group's q | k | v columns (G*D/2 q pairs,
+  // D/2 k pairs, D/2 v pairs): all its split partials and its RoPE pair are
+  // requested here, after the block ids and before the tile loads, so the
+  // tile loads wait only for the block ids and the sums below only for these
+  // loads -- one round trip instead of one per split.  Loads are unconditional
+  // (clamped item and split indexes); the extras are dropped.
+  constexpr int SB = 8;                    // split partials requested at once
+  const int nq = G * (D / 2);
+  const int nitems = nq + D;
+  const int pr = min(max(pos, 0), p.rope_len - 1);
+  const float* part = p.part + (size_t)b * N;
+  const size_t sstride = (size_t)p.B * N;
+  auto item_col = [&](int it, int& d2) {   // output column of item it, and its rotation pair index
+    if (it < nq) {
+      d2 = it % (D / 2);
+      return (kvh * G + it / (D / 2)) * D + 2 * d2;
+    }
+    if (it < nq + D / 2) {
+      d2 = it - nq;
+      return p.Hq * D + kvh * D + 2 * d2;
+    }
+    d2 = it - nq - D / 2;
+    return (p.Hq + p.Hkv) * D + kvh * D + 2 * d2;
+  };
+  auto load_parts = [&](int n, int s0, float2 (&pv)[SB]) {
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      pv[s] = *reinterpret_cast<const float2*>(part + (size_t)min(s0 + s, p.splits - 1) * sstride + n);
+  };
+  int d2_0;
+  const int n0 = item_col(min(tid, nitems - 1), d2_0);
+  float2 pv0[SB];
+  load_parts(n0, 0, pv0);
+  const float2 cs0 = *reinterpret_cast<const float2*>(p.rope + ((size_t)pr * (D / 2) + d2_0) * 2);
+
   // The first tiles' K / V loads depend only on the block table: issue them
-  // before the q / k / v prologue so their latency overlaps it (tile 0 of the
-  // wave is a valid address even when the wave has no tile; it is not used).
+  // before the prologue's arithmetic so their latency overlaps it (tile 0 of
+  // the wave is a valid address even when the wave has no tile; it is not used).
   Tile t[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) load(min(i, max(nt, 1) - 1), 0, t[i]);
 
-  // ---- q, k, v of the new token -----------------------------------------
+  // ---- q, k, v of the new token: sums, RoPE, stores --------------------------
   long long slot = -1;
   if (pos >= 0 && pos / bs < p.bt_stride) {
     const int blk = bt[pos / bs];
     if (blk >= 0 && blk < p.num_blocks) slot = (long long)blk * bs + pos % bs;
   }
   {
-    const int nq = G * (D / 2);
-    const int pr = min(max(pos, 0), p.rope_len - 1);
-    const float* part = p.part + (size_t)b * N;
-    const size_t sstride = (size_t)p.B * N;
-    for (int it = tid; it < nq + D; it += 64 * NW) {
-      int n, d2;
-      if (it < nq) {
-        d2 = it % (D / 2);
-        n = (kvh * G + it / (D / 2)) * D + 2 * d2;
-      } else if (it < nq + D / 2) {
-        d2 = it - nq;
-        n = p.Hq * D + kvh * D + 2 * d2;
-      } else {
-        d2 = it - nq - D / 2;
-        n = (p.Hq + p.Hkv) * D + kvh * D + 2 * d2;
-      }
-      float v0 = 0.0f, v1 = 0.0f;
-      for (int s = 0; s < p.splits; ++s) {
-        const float2 pv = *reinterpret_cast<const float2*>(part + s * sstride + n);
-        v0 += pv.x;
-        v1 += pv.y;
-      }
+    auto finish_item = [&](int it, int d2, float v0, float v1, float2 cs) {
       if (it < nq + D / 2) {
-        const float2 cs = *reinterpret_cast<const float2*>(p.rope + ((size_t)pr * (D / 2) + d2) * 2);
         const float a = v0 * cs.x - v1 * cs.y;
         const float c2 = v0 * cs.y + v1 * cs.x;
         v0 = a;
@@ -167,6 +181,43 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
         if (p.write_before && slot >= 0)
           *reinterpret_cast<uint32_t*>((it < nq + D / 2 ? kcache : vcache) + (size_t)slot * rs + 2 * d2) = w;
       }
+    };
+    // splits summed in order 0, 1, 2, ... whichever batch they arrive in
+    auto sum_item = [&](int n, const float2 (&first)[SB], float& v0, float& v1) {
+      v0 = 0.0f;
+      v1 = 0.0f;
+#pragma unroll
+      for (int s = 0; s < SB; ++s)
+        if (s < p.splits) {
+          v0 += first[s].x;
+          v1 += first[s].y;
+        }
+      for (int s0 = SB; s0 < p.splits; s0 += SB) {
+        float2 pv[SB];
+        load_parts(n, s0, pv);
+#pragma unroll
+        for (int s = 0; s < SB; ++s)
+          if (s0 + s < p.splits) {
+            v0 += pv[s].x;
+            v1 += pv[s].y;
+          }
+      }
+    };
+    if (tid < nitems) {
+      float v0, v1;
+      sum_item(n0, pv0, v0, v1);
+      finish_item(tid, d2_0, v0, v1, cs0);
+    }
+    // items beyond the first of a thread (head_dim 128, or large groups)
+    for (int it = tid + 64 * NW; it < nitems; it += 64 * NW) {
+      int d2;
+      const int n = item_col(it, d2);
+      float2 pv[SB];
+      load_parts(n, 0, pv);
+      const float2 cs = *reinterpret_cast<const float2*>(p.rope + ((size_t)pr * (D / 2) + d2) * 2);
+      float v0, v1;
+      sum_item(n, pv, v0, v1);
+      finish_item(it, d2, v0, v1, cs);
     }
     for (int it = tid; it < (16 - G) * (D / 2); it += 64 * NW)
       *reinterpret_cast<uint32_t*>(&sq[G * D + 2 * it]) = 0u;
