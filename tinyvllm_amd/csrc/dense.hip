@@ -415,13 +415,33 @@ __global__ void __launch_bounds__(256) qkv_rope_kernel(const QKVParams p) {
   if (t >= (long long)p.M * half) return;
   const int m = (int)(t / half);
   const int n = 2 * (int)(t - (long long)m * half);
-  float v0 = 0.0f, v1 = 0.0f;
-  for (int s = 0; s < p.splits; ++s) {
-    const float2 pv = *reinterpret_cast<const float2*>(p.part + ((size_t)s * p.M + m) * N + n);
-    v0 += pv.x;
-    v1 += pv.y;
-  }
+  // SB split partials requested at once with the position (one round trip
+  // for the usual split counts); indexes past the last split re-read it and
+  // are dropped; the sum runs in split order
+  constexpr int SB = 8;
+  float2 pv[SB];
+#pragma unroll
+  for (int s = 0; s < SB; ++s)
+    pv[s] = *reinterpret_cast<const float2*>(p.part + ((size_t)min(s, p.splits - 1) * p.M + m) * N + n);
   const int pos = p.positions ? p.positions[m] : p.pos_base + m;
+  float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+  for (int s = 0; s < SB; ++s)
+    if (s < p.splits) {
+      v0 += pv[s].x;
+      v1 += pv[s].y;
+    }
+  for (int s0 = SB; s0 < p.splits; s0 += SB) {
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      pv[s] = *reinterpret_cast<const float2*>(p.part + ((size_t)min(s0 + s, p.splits - 1) * p.M + m) * N + n);
+#pragma unroll
+    for (int s = 0; s < SB; ++s)
+      if (s0 + s < p.splits) {
+        v0 += pv[s].x;
+        v1 += pv[s].y;
+      }
+  }
   if (n < qn + kn) {
     const int i = (n % p.D) >> 1;
     const int pr = min(max(pos, 0), p.rope_len - 1);
@@ -491,7 +511,16 @@ __global__ void __launch_bounds__(64) advance_kernel(const AdvanceParams p) {
   const int m = blockIdx.x;
   const int lane = threadIdx.x;
   unsigned long long best = 0;
-  for (int j = lane; j < p.nparts; j += 64) best = max(best, p.keys[(size_t)j * p.M + m]);
+  // U keys per lane requested at once (500 per sequence at a 32000 vocabulary:
+  // one round trip); indexes past the last key re-read it, which max ignores
+  constexpr int U = 8;
+  for (int j0 = 0; j0 < p.nparts; j0 += 64 * U) {
+    unsigned long long kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) kv[u] = p.keys[(size_t)min(j0 + lane + 64 * u, p.nparts - 1) * p.M + m];
+#pragma unroll
+    for (int u = 0; u < U; ++u) best = max(best, kv[u]);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute((lane ^ off) << 2, (int)(uint32_t)best);
