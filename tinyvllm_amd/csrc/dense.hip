@@ -328,9 +328,13 @@ __global__ void __launch_bounds__(256) norm_kernel(const NormParams p) {
       v[i] = *reinterpret_cast<const f32x4*>(x + k);
     }
     if constexpr (MODE == kNormPart) {
+      if (p.splits == 1) {   // unsplit producer (prompt passes): one load, not SB copies of it
+        t[0][i] = *reinterpret_cast<const f32x4*>(p.part + (size_t)m * p.dim + k);
+      } else {
 #pragma unroll
-      for (int u = 0; u < SB; ++u)
-        t[u][i] = *reinterpret_cast<const f32x4*>(p.part + ((size_t)min(u, p.splits - 1) * p.M + m) * p.dim + k);
+        for (int u = 0; u < SB; ++u)
+          t[u][i] = *reinterpret_cast<const f32x4*>(p.part + ((size_t)min(u, p.splits - 1) * p.M + m) * p.dim + k);
+      }
     }
   }
   if constexpr (MODE == kNormPart) {
@@ -420,9 +424,13 @@ __global__ void __launch_bounds__(256) qkv_rope_kernel(const QKVParams p) {
   // are dropped; the sum runs in split order
   constexpr int SB = 8;
   float2 pv[SB];
+  if (p.splits == 1) {   // unsplit producer (prompt passes): one load, not SB copies of it
+    pv[0] = *reinterpret_cast<const float2*>(p.part + (size_t)m * N + n);
+  } else {
 #pragma unroll
-  for (int s = 0; s < SB; ++s)
-    pv[s] = *reinterpret_cast<const float2*>(p.part + ((size_t)min(s, p.splits - 1) * p.M + m) * N + n);
+    for (int s = 0; s < SB; ++s)
+      pv[s] = *reinterpret_cast<const float2*>(p.part + ((size_t)min(s, p.splits - 1) * p.M + m) * N + n);
+  }
   const int pos = p.positions ? p.positions[m] : p.pos_base + m;
   float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
