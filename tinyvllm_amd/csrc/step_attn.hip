@@ -382,15 +382,17 @@ bool step_attn_supported(int head_dim, int group, int block_size) {
 }
 
 #ifndef TV_STEP_ATTN_W64
-#define TV_STEP_ATTN_W64 8    // waves per work-group at head_dim 64
+#define TV_STEP_ATTN_W64 6    // waves per work-group at head_dim 64
 #endif
 #ifndef TV_STEP_ATTN_PF64
 #define TV_STEP_ATTN_PF64 2   // tiles in flight per wave at head_dim 64
 #endif
 
-// head_dim 64: 8 waves (two per SIMD with one work-group per CU at batch 64 x 4
-// KV heads) and two tiles in flight per wave; head_dim 128: 4 waves, whose
-// larger tiles need more than the 256 registers two waves per SIMD allow.
+// head_dim 64: 6 waves and two tiles in flight per wave (TinyLlama step, batch
+// 64 x 4 KV heads, one work-group per CU: 1480 us/step against 1482 with one
+// tile in flight, 1487 with 8 waves and one tile, 1496 with 8 waves and two,
+// 1543 with 12, 1548 with 16); head_dim 128: 4 waves, whose larger tiles need
+// more than the 256 registers two waves per SIMD allow.
 void launch_step_attn(const StepAttnParams& p, int head_dim, int dtype, hipStream_t s) {
   constexpr int W64 = TV_STEP_ATTN_W64, PF64 = TV_STEP_ATTN_PF64;
   const dim3 grid(p.Hkv, p.B);
