@@ -705,7 +705,13 @@ void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) 
   hipLaunchKernelGGL((prefill_fa_kernel<T, D, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN, PAGED>), grid,
                      dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
 #else
-  if (cfg == 0) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, BN, PAGED>), grid, dim3(512), 0, stream, pp);
+  if constexpr (D == 64) {
+    if (cfg == 3) {
+      hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 4, 32, PAGED>), grid, dim3(1024), 0, stream, pp);
+      return;
+    }
+  }
+  if (cfg == 0 || cfg == 3) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, BN, PAGED>), grid, dim3(512), 0, stream, pp);
   else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, 32, PAGED>), grid, dim3(512), 0, stream, pp);
   else hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 1, BN, PAGED>), grid, dim3(256), 0, stream, pp);
 #endif
@@ -799,7 +805,12 @@ int launch_flash_prefill_paged(const PrefillParams& p_in, int dtype, hipStream_t
   const dim3 grid(pp.num_heads, units);
   const long long wgs = (long long)grid.x * grid.y;
   const bool long_rows = prefill_key_tiles_host(pp, (pp.q_len + kPrefillBM - 1) / kPrefillBM - 1) >= 8;
-  const int cfg = long_rows && wgs <= 256 ? 0 : (d64 && long_rows && wgs < 1024 ? 2 : 1);
+  // At head_dim 64 a one-per-CU grid of long rows takes four key groups of
+  // 32-key tiles here (a 512-row chunk over 3584 cached tokens, TinyLlama
+  // heads: 34.7 against 36.6 us with two groups of 64-key tiles); prompts
+  // without a prefix keep two groups, which were faster at L = 512.
+  int cfg = long_rows && wgs <= 256 ? 0 : (d64 && long_rows && wgs < 1024 ? 2 : 1);
+  if (cfg == 0 && d64) cfg = 3;
   if (dtype == kF16) {
     if (d64) launch_fa<_Float16, 64, true>(cfg, grid, pp, stream);
     else launch_fa<_Float16, 128, true>(cfg, grid, pp, stream);
