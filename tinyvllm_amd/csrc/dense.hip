@@ -239,6 +239,20 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
     storeA(ar[0], av[0], 0);
     lds_barrier();
     compute(w[0], 0);
+  } else if (NWS >= 2 && nc == 2) {
+    // both chunks requested at once, one in each LDS buffer: one round trip
+    // instead of the pipeline's two (the Wqkv product of the decode step)
+    u32x4 a1[8];
+    bool v1;
+    loadW(0, w[0]);
+    loadW(1, w[1 % NWS]);
+    loadA(0, ar[0], av[0]);
+    loadA(1, a1, v1);
+    storeA(ar[0], av[0], 0);
+    storeA(a1, v1, 1);
+    lds_barrier();
+    compute(w[0], 0);
+    compute(w[1 % NWS], 1);
   } else {
 #pragma unroll
     for (int i = 0; i < NWS - 1; ++i) loadW(i, w[i]);
