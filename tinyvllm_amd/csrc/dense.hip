@@ -78,6 +78,10 @@ template <> __device__ __forceinline__ f32x4 mfma_frag<float>(u32x4 a, u32x4 b, 
 #ifndef TV_LINEAR_WSTAGES
 #define TV_LINEAR_WSTAGES 2
 #endif
+// A chunks requested ahead of the one being multiplied.  Two ahead measured
+// slower for every product of the TinyLlama batch-64 decode step (64-step
+// graph: 1468 us/step at one ahead; two ahead for the SwiGLU product 1488, for
+// the split-K partial products 1485, for both 1505), so one it is.
 #ifndef TV_LINEAR_ASTAGES
 #define TV_LINEAR_ASTAGES 1
 #endif
