@@ -46,6 +46,21 @@
 // per SIMD, ~1.1 us per tile step against ~1.5 us for two waves' steps
 // together).  Two independent work-groups per CU, drifting out of phase, are
 // what keeps the matrix pipes busiest here.
+//
+// Where the time goes (L 2048 / 4096 / 8192, same heads).  Copies of this
+// kernel that skip work, timed: without the K and V fragment reads from LDS no
+// faster (LDS bandwidth is not the limit); without the tile loads into LDS 15-20%
+// faster (53 / 163 / 515 us against 62 / 202 / 645 us).  Requesting the tiles
+// four ahead instead of three (five buffers, 2 x 80 KB per CU) changes nothing,
+// and the tile descriptors advanced by 64-bit adds instead of recomputed with
+// 64-bit multiplies gave ~3% (about 50 fewer scalar instructions per step).  L2
+// serves the K / V re-reads (95.6% hit rate at L 8192; FETCH_SIZE about the
+// unique input bytes).  A software-pipelined form -- the scores of tile j + 1
+// formed while tile j's softmax runs, exponentials and V reads interleaved
+// between the score and P V products with sched_group_barrier, O kept in one
+// register set by sending every tile through one code path -- was correct and
+// cut the waits for LDS data 3x, but the time moved to the barrier: 63 / 200 /
+// 635 us against 60 / 198 / 630 us.
 #include "tv_common.h"
 #include "tv_params.h"
 
@@ -58,6 +73,7 @@ namespace {
 constexpr int kRowsBM = 128;   // query rows per work-group
 constexpr int kRowsBN = 32;    // keys per tile
 constexpr int kRowsBuf = 4;    // tile buffers
+static_assert(kRowsBuf == 4 || kRowsBuf == 5, "the step loop is unrolled for 4 or 5 buffers");
 
 // chunk permutation of tile row r (16-byte chunks; 16 per row at head_dim 128,
 // 8 at 64): distinct over any 16 consecutive rows for a fixed chunk (K reads),
@@ -190,13 +206,26 @@ prefill_rows_kernel(const PrefillParams pa) {
   }
   // tile t (clamped to the last tile) into buffer t % NB; the resource's range
   // ends at the last key row
+  // Tile t's K / V buffer descriptors (base at the tile's first key row,
+  // range ending at the last key row).  Tiles are requested in order t = 0, 1,
+  // 2, ...; each request advances the descriptors by one tile (64-bit adds,
+  // no per-request multiplies on the scalar unit), and from t = ntiles on the
+  // last tile is requested again.
+  unsigned long long ka = reinterpret_cast<unsigned long long>(kbase);
+  unsigned long long va = reinterpret_cast<unsigned long long>(vbase);
+  unsigned long long kr = (unsigned long long)(klim - 1) * kstr + D * sizeof(T);
+  unsigned long long vr = (unsigned long long)(klim - 1) * vstr + D * sizeof(T);
+  const unsigned long long kstep = (unsigned long long)BN * kstr;
+  const unsigned long long vstep = (unsigned long long)BN * vstr;
   auto issue = [&](int t) {
-    const int tc = min(t, ntiles - 1);
-    const unsigned long long r0 = (unsigned long long)tc * BN;
-    const unsigned long long kb = ((unsigned long long)(klim - 1) - r0) * kstr + D * sizeof(T);
-    const unsigned long long vb = ((unsigned long long)(klim - 1) - r0) * vstr + D * sizeof(T);
-    const u32x4 rk = rsrc_words(kbase + r0 * kstr, kb);
-    const u32x4 rv = rsrc_words(vbase + r0 * vstr, vb);
+    if (t > 0 && t < ntiles) {
+      ka += kstep;
+      kr -= kstep;
+      va += vstep;
+      vr -= vstep;
+    }
+    const u32x4 rk = rsrc_words(reinterpret_cast<const void*>(ka), kr);
+    const u32x4 rv = rsrc_words(reinterpret_cast<const void*>(va), vr);
     const uint32_t buf = lds0 + (uint32_t)((t % NB) * BUFB);
 #pragma unroll
     for (int i = 0; i < NI; ++i) load_lds16(rk, sgpr(buf + (uint32_t)((wave * NI + i) * 1024)), kvoff[i]);
@@ -212,9 +241,8 @@ prefill_rows_kernel(const PrefillParams pa) {
   // zeroed so nothing non-finite can reach a masked product.
   for (int i = threadIdx.x; i < NB * BUFB / 16; i += 256) reinterpret_cast<u32x4*>(smem)[i] = u32x4{0, 0, 0, 0};
   lds_barrier();
-  issue(0);
-  issue(1);
-  issue(2);
+#pragma unroll
+  for (int t = 0; t < NB - 1; ++t) issue(t);
 
   // fragment read offsets inside a buffer (bytes).  chunk_perm(r + 16) ==
   // chunk_perm(r), so the second 16-key block and the upper 16 V rows are the
@@ -297,9 +325,9 @@ prefill_rows_kernel(const PrefillParams pa) {
   const bool idle = row0 >= p.q_len;       // rows past the prompt: nothing to compute
   auto step = [&](auto bufc, int jj) {
     constexpr int B = decltype(bufc)::value;
-    wait_vmcnt<4 * NI>();        // this wave's loads of tile jj are in LDS (tiles jj+1, jj+2 may fly)
+    wait_vmcnt<2 * NI * (NB - 2)>();   // this wave's loads of tile jj are in LDS (tiles jj+1 .. jj+NB-2 may fly)
     lds_barrier();               // every wave's; and every wave is done with tile jj-1's buffer
-    issue(jj + 3);
+    issue(jj + NB - 1);
     const int k0 = jj * BN;
     if (idle || (p.causal && k0 > row0 + 31)) return;   // nothing visible in the tile
     const uint8_t* sb = smem + B * BUFB;
@@ -343,6 +371,8 @@ prefill_rows_kernel(const PrefillParams pa) {
     if (jj + 1 < ntiles) step(std::integral_constant<int, 1>{}, jj + 1);
     if (jj + 2 < ntiles) step(std::integral_constant<int, 2>{}, jj + 2);
     if (jj + 3 < ntiles) step(std::integral_constant<int, 3>{}, jj + 3);
+    if constexpr (NB > 4)
+      if (jj + 4 < ntiles) step(std::integral_constant<int, NB - 1>{}, jj + 4);
   }
   wait_vmcnt<0>();               // the clamped trailing loads land before the work-group ends
 
