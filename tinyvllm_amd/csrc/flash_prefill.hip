@@ -102,29 +102,6 @@ __device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v, int out_
 // and loaded two steps ahead through buffer loads whose range ends at the last
 // key row (rows past kv_len read as zero), one barrier per step.
 
-template <typename T> __device__ __forceinline__ u32x4 scale8(u32x4 w, float c) {
-  u32x4 r;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float a, b;
-    unpack2<T>(w[k], a, b);
-    r[k] = pack2<T>(a * c, b * c);
-  }
-  return r;
-}
-
-// Where the softmax scale enters.  fp16: Q is pre-scaled by scale * log2(e)
-// and rounded to fp16 once (a relative error of at most 2^-11 per element,
-// comparable to the rounding of the fp16 inputs themselves), and the score
-// accumulator starts at -m, so scores leave the matrix cores ready for exp2.
-// bf16: rounding q * scale to bf16 would add up to 2^-8 relative error to
-// every score (scores of tens of units then move the softmax by several
-// percent), so Q stays as given, the accumulator starts at 0 and each score
-// takes one fp32 fma, s * scale * log2(e) - m -- the reference's order, the
-// scale applied after the product (llama.py:84).
-template <typename T> constexpr bool kPreScaleQ = false;
-template <> constexpr bool kPreScaleQ<_Float16> = true;
-
 template <typename T> constexpr uint32_t kOnes2 = 0;
 template <> constexpr uint32_t kOnes2<_Float16> = 0x3C003C00u;
 template <> constexpr uint32_t kOnes2<__bf16> = 0x3F803F80u;

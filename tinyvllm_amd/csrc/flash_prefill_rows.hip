@@ -104,8 +104,14 @@ __device__ __forceinline__ uint32_t sgpr(uint32_t x) { return __builtin_amdgcn_r
 
 __device__ __forceinline__ u32x4 rsrc_words(const void* base, unsigned long long bytes) {
   const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-  const uint32_t n = bytes >> 32 ? 0xffffffffu : (uint32_t)bytes;
-  return u32x4{sgpr((uint32_t)a), sgpr((uint32_t)(a >> 32)), sgpr(n), 0x00020000u};
+  // range clamped to 32 bits with a scalar compare of the high word (as C the
+  // compiler makes it a 64-bit vector compare plus readfirstlane)
+  uint32_t n;
+  asm("s_cmp_lg_u32 %1, 0\n\ts_cselect_b32 %0, -1, %2"
+      : "=s"(n)
+      : "s"((uint32_t)(bytes >> 32)), "s"((uint32_t)bytes)
+      : "scc");
+  return u32x4{sgpr((uint32_t)a), sgpr((uint32_t)(a >> 32)), n, 0x00020000u};
 }
 
 template <typename T> constexpr uint32_t kRowsOnes2 = 0;
@@ -182,9 +188,10 @@ prefill_rows_kernel(const PrefillParams pa) {
       qi[r] = row0 + r * 16 + col;
 #pragma unroll
       for (int ks = 0; ks < KSD; ++ks) {
-        qf[r][ks] = qi[r] < p.q_len
-                        ? *reinterpret_cast<const u32x4*>(qg + (size_t)qi[r] * p.q_stride + ks * 32 + g * 8)
-                        : u32x4{0, 0, 0, 0};
+        const u32x4 raw = qi[r] < p.q_len
+                              ? *reinterpret_cast<const u32x4*>(qg + (size_t)qi[r] * p.q_stride + ks * 32 + g * 8)
+                              : u32x4{0, 0, 0, 0};
+        qf[r][ks] = kPreScaleQ<T> ? scale8<T>(raw, c) : raw;
       }
     }
   }
@@ -263,6 +270,7 @@ prefill_rows_kernel(const PrefillParams pa) {
   f32x4 oacc[RB][DB];
   float lpart[RB];      // this lane's share of the row sum (keys 4g..4g+3 of every 16)
   float mref[RB], thr[RB];
+  f32x4 negm[RB];       // -m in every element: the fp16 score accumulator's initial value
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
 #pragma unroll
@@ -270,18 +278,21 @@ prefill_rows_kernel(const PrefillParams pa) {
     lpart[r] = 0.0f;
     mref[r] = 0.0f;
     thr[r] = -__FLT_MAX__;
+    negm[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // raw scores of a tile starting at key k0 -> log2 domain relative to the
-  // running maximum (one fma), masked, rescaled when a row's maximum moved by
-  // more than 8
+  // scores of a tile starting at key k0 -> log2 domain relative to the running
+  // maximum (fp16: already, from the pre-scaled Q and the -m accumulator; bf16:
+  // one fma), masked, rescaled when a row's maximum moved by more than 8
   auto softmax = [&](f32x4 (&st)[RB][KB], int k0) {
+    if constexpr (!kPreScaleQ<T>) {
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
+      for (int r = 0; r < RB; ++r)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[r][kb][i] = fmaf(st[r][kb][i], c, -mref[r]);
+          for (int i = 0; i < 4; ++i) st[r][kb][i] = fmaf(st[r][kb][i], c, -mref[r]);
+    }
     if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0))) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
@@ -296,10 +307,12 @@ prefill_rows_kernel(const PrefillParams pa) {
     bool need_any = false;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      float t0 = fmaxf(fmaxf(st[r][0][0], st[r][0][1]), fmaxf(st[r][0][2], st[r][0][3]));
+      // a chain of three-input maxima (v_max3_f32): the 4 KB values (an even
+      // count) as one pair, then two more per step
+      static_assert((4 * KB) % 2 == 0, "pairs");
+      float t0 = fmaxf(st[r][0][0], st[r][0][1]);
 #pragma unroll
-      for (int kb = 1; kb < KB; ++kb)
-        t0 = fmaxf(t0, fmaxf(fmaxf(st[r][kb][0], st[r][kb][1]), fmaxf(st[r][kb][2], st[r][kb][3])));
+      for (int j = 2; j < 4 * KB; j += 2) t0 = fmaxf(t0, fmaxf(st[r][j >> 2][j & 3], st[r][(j + 1) >> 2][(j + 1) & 3]));
       lm[r] = t0;
       need_any = need_any || lm[r] > thr[r];
     }
@@ -318,6 +331,7 @@ prefill_rows_kernel(const PrefillParams pa) {
         for (int kb = 0; kb < KB; ++kb) st[r][kb] -= delta;
         mref[r] += delta;
         thr[r] = need ? 8.0f : thr[r];
+        if constexpr (kPreScaleQ<T>) negm[r] = f32x4{-mref[r], -mref[r], -mref[r], -mref[r]};
       }
     }
   };
@@ -342,7 +356,7 @@ prefill_rows_kernel(const PrefillParams pa) {
     for (int r = 0; r < RB; ++r)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        st[r][kb] = mfma16x16x32<T>(kf[kb][0], qf[r][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        st[r][kb] = mfma16x16x32<T>(kf[kb][0], qf[r][0], kPreScaleQ<T> ? negm[r] : f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int ks = 1; ks < KSD; ++ks) st[r][kb] = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], st[r][kb]);
       }

@@ -118,6 +118,30 @@ template <> __device__ __forceinline__ uint32_t pack2<__bf16>(float a, float b) 
   return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
 }
 
+// Eight packed 16-bit values each multiplied by c (fp32 product, rounded back).
+template <typename T> __device__ __forceinline__ u32x4 scale8(u32x4 w, float c) {
+  u32x4 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float a, b;
+    unpack2<T>(w[k], a, b);
+    r[k] = pack2<T>(a * c, b * c);
+  }
+  return r;
+}
+
+// Where the softmax scale enters in the prefill kernels.  fp16: Q is
+// pre-scaled by scale * log2(e) and rounded to fp16 once (a relative error of
+// at most 2^-11 per element, comparable to the rounding of the fp16 inputs
+// themselves), and the score accumulator starts at -m, so scores leave the
+// matrix cores ready for exp2.  bf16: rounding q * scale to bf16 would add up
+// to 2^-8 relative error to every score (scores of tens of units then move the
+// softmax by several percent), so Q stays as given, the accumulator starts at 0
+// and each score takes one fp32 fma, s * scale * log2(e) - m -- the
+// reference's order, the scale applied after the product (llama.py:84).
+template <typename T> inline constexpr bool kPreScaleQ = false;
+template <> inline constexpr bool kPreScaleQ<_Float16> = true;
+
 // max over the four lanes l, l^16, l^32, l^48 (one query column of the S^T
 // accumulator) with gfx950 row / half-wave swaps (VALU, no LDS round trip).
 __device__ __forceinline__ float max_over_g(float x) {
