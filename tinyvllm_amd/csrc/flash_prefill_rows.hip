@@ -29,13 +29,14 @@
 // query at the end.
 //
 // Measured on MI355X (Llama-3-8B heads, Hq 32 / Hkv 8, head_dim 128, fp16,
-// causal): L 2048 62-64 us against 64-68 for the 64-row kernel, L 4096 178-185
-// against 207-210; at L <= 1024 and at head_dim 64 the 64-row kernel is faster
-// (more, shorter work-groups), so the launcher uses this one only for long
+// causal): L 2048 58 us (53-54 us replayed in a graph) against 64-68 for the
+// 64-row kernel, L 4096 ~195 against 207-210; at L <= 1024 and at head_dim 64
+// the 64-row kernel is faster (L 512 / 1024 at head_dim 64: 7.6 / 13.0 us
+// against 12.1 / 20.7), so the launcher uses this one only for long
 // head_dim-128 prompts.  A tile step of the longest work-group takes ~2000
 // cycles against 512 of MFMA work (clock stamps): the LDS-DMA issue, LDS read
 // issue, score wait and softmax are serial within a wave, and with 2 waves per
-// SIMD (208 VGPRs) little of it overlaps.  Splitting a work-group's key tiles
+// SIMD (196 VGPRs fp16, 206 bf16) little of it overlaps.  Splitting a work-group's key tiles
 // over two 4-wave groups in ping-pong (one group's MFMA phase against the
 // other's softmax phase, a barrier per phase) was correct but 2x slower: the
 // softmax phase of one wave ran ~4x longer while the other issued MFMAs.
