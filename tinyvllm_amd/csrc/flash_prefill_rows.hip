@@ -45,8 +45,14 @@
 // work-group (both waves of a SIMD then pass the same barrier, in phase) or
 // run back to back by one work-group (one work-group per CU leaves one wave
 // per SIMD, ~1.1 us per tile step against ~1.5 us for two waves' steps
-// together).  Two independent work-groups per CU, drifting out of phase, are
-// what keeps the matrix pipes busiest here.
+// together).  Nor did balancing inside each wave (16 rows of 64-row tile i and
+// 16 of tile n - 1 - i, the first block skipped past its diagonal; every
+// work-group the same causal work, 2 per CU): 59.3 / 211 us at L 2048 / 4096
+// against 57.1 / 192.  The work-group holding the last rows still walks every
+// key tile (64 at L 2048), and a one-block step beside another work-group
+// costs about what a two-block step costs alone, so the longest chain of
+// steps, not the total work, sets the time.  Two independent work-groups per
+// CU, drifting out of phase, are what keeps the matrix pipes busiest here.
 //
 // Where the time goes (L 2048 / 4096 / 8192, same heads).  Copies of this
 // kernel that skip work, timed: without the K and V fragment reads from LDS no
