@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from oracle.attention import flash_prefill_ref
+from tests.random_cases import case_count, case_seed
 
 pytestmark = pytest.mark.gpu
 
@@ -218,8 +219,9 @@ def test_mfma_split_rows_merge(chunk_tiles, lq, causal, dtype):
 
 # ---- seeded random shapes -------------------------------------------------------------
 
-def _random_prefill_cases(n=24, seed=71):
-    rng = np.random.Generator(np.random.PCG64(seed))
+def _random_prefill_cases(n=None, seed=71):
+    n = case_count(24) if n is None else n
+    rng = np.random.Generator(np.random.PCG64(case_seed(seed)))
     cases = []
     for i in range(n):
         hkv = int(rng.choice([1, 2, 4, 8]))
@@ -279,6 +281,28 @@ def test_varlen_matches_per_prompt(lens, hq, hkv, d, causal, dtype):
         single = flash(q[sl], k[sl], v[sl], causal).float().cpu().numpy()
         assert np.abs(got[sl] - single).max() <= TOL[dtype], (n, s)
         s += n
+
+
+def _random_varlen_cases(n=None, seed=73):
+    n = case_count(8) if n is None else n
+    rng = np.random.Generator(np.random.PCG64(case_seed(seed)))
+    cases = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        hq = hkv * int(rng.choice([1, 2, 4, 8]))
+        d = int(rng.choice([64, 128]))
+        lens = [int(x) for x in rng.integers(1, 700, int(rng.integers(1, 6)))]
+        causal = bool(rng.random() < 0.7)
+        dtype = [torch.float16, torch.bfloat16][int(rng.integers(0, 2))]
+        cases.append((i, lens, hq, hkv, d, causal, dtype))
+    return cases
+
+
+@pytest.mark.parametrize("i,lens,hq,hkv,d,causal,dtype", _random_varlen_cases())
+def test_random_varlen(i, lens, hq, hkv, d, causal, dtype):
+    """Seeded random packs of 1-5 prompts (lengths 1-699), GQA shapes, head
+    dims, masks and dtypes: every prompt equals the oracle and its own launch."""
+    test_varlen_matches_per_prompt(lens, hq, hkv, d, causal, dtype)
 
 
 def test_varlen_fp32_output_and_strided_inputs():
@@ -375,6 +399,30 @@ def test_paged_prefill_equals_last_rows_of_whole_prompt(dtype, d, hq, hkv, start
     want = flash_prefill_ref(q[start:].float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None],
                              causal, q_offset=start)[0]
     assert np.abs(out[0].float().cpu().numpy() - want).max() <= TOL[dtype]
+
+
+def _random_paged_prefill_cases(n=None, seed=77):
+    n = case_count(8) if n is None else n
+    rng = np.random.Generator(np.random.PCG64(case_seed(seed)))
+    cases = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        hq = hkv * int(rng.choice([1, 2, 4, 8]))
+        d = int(rng.choice([64, 128]))
+        bs = int(rng.choice([4, 8, 16, 16, 32]))
+        start = int(rng.integers(0, 1500))
+        n_rows = int(rng.integers(1, 400))
+        causal = bool(rng.random() < 0.8)
+        dtype = [torch.float16, torch.bfloat16][int(rng.integers(0, 2))]
+        cases.append((i, dtype, d, hq, hkv, start, n_rows, bs, causal))
+    return cases
+
+
+@pytest.mark.parametrize("i,dtype,d,hq,hkv,start,n,bs,causal", _random_paged_prefill_cases())
+def test_random_paged_prefill(i, dtype, d, hq, hkv, start, n, bs, causal):
+    """Seeded random chunks (start 0-1499, 1-399 rows) over shuffled block pools
+    of block size 4-32: the chunk equals the last rows of the whole prompt."""
+    test_paged_prefill_equals_last_rows_of_whole_prompt(dtype, d, hq, hkv, start, n, bs, causal)
 
 
 def test_paged_prefill_invalid_block_id_gives_nan():

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle.attention import paged_decode_ref
+from tests.random_cases import case_count, case_seed
 
 pytestmark = pytest.mark.gpu
 
@@ -276,8 +277,9 @@ def test_rejects_bad_arguments():
 
 # ---- seeded random shapes -------------------------------------------------------------
 
-def _random_decode_cases(n=24, seed=81):
-    rng = np.random.Generator(np.random.PCG64(seed))
+def _random_decode_cases(n=None, seed=81):
+    n = case_count(24) if n is None else n
+    rng = np.random.Generator(np.random.PCG64(case_seed(seed)))
     cases = []
     for i in range(n):
         hkv = int(rng.choice([1, 2, 4, 8]))
