@@ -17,6 +17,11 @@ Follows tinyvllm/model/llama.py step by step:
 * greedy sampling       sample_tokens with temperature 0 -> argmax, sampling.py:131-134
 * ``round_bf16``        storage rounding of a bfloat16 cache (no reference counterpart:
                         the reference has no bfloat16, weights.py:44)
+* ``act_dtype``         (LlamaRef option, no reference counterpart) rounds the activations
+                        a 16-bit model stores between its kernels -- each product's
+                        normalised input, q / k / v after RoPE, the attention output and
+                        the SwiGLU output -- through that dtype; unset, every activation
+                        stays float32 as in the reference
 
 Arithmetic is float32 (the precision the fp16 / bf16 kernels are held to); the paged cache stores
 ``cache_dtype`` (float16 by default, as KVCache(dtype=float16), kv_cache.py:25-32).
@@ -75,14 +80,26 @@ def greedy_ref(logits):
 class LlamaRef:
     """The reference model's forward passes over numpy float32 weights."""
 
-    def __init__(self, cfg, weights, cache_dtype=np.float16):
+    def __init__(self, cfg, weights, cache_dtype=np.float16, act_dtype=None):
         """``cache_dtype``: a numpy dtype the cache rows are rounded through, or
-        ``"bfloat16"`` (rounded with ``round_bf16``)."""
+        ``"bfloat16"`` (rounded with ``round_bf16``).  ``act_dtype`` (same forms;
+        None keeps float32): the storage type of the activations between kernels."""
         self.cfg = cfg
         self.w = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
         self.cache_dtype = cache_dtype
+        self.act_dtype = act_dtype
         self.head_dim = cfg.dim // cfg.n_heads
         self.cos, self.sin = rope_tables_ref(self.head_dim, cfg.max_seq_len * 2, cfg.rope_theta)
+
+    def _round(self, x, dtype):
+        if dtype is None:
+            return np.asarray(x, dtype=np.float32)
+        if isinstance(dtype, str) and dtype == "bfloat16":
+            return round_bf16(x)
+        return np.asarray(x).astype(dtype).astype(np.float32)
+
+    def _act(self, x):
+        return self._round(x, self.act_dtype)
 
     def _lin(self, x, name):
         return (x @ self.w[name].T).astype(np.float32)
@@ -91,31 +108,28 @@ class LlamaRef:
         """Projections + RoPE of tokens x [T, dim] at positions pos [T] (llama.py:178-182, 315-322)."""
         c, d = self.cfg, self.head_dim
         p = f"layers.{i}."
-        xn = rms_norm_ref(x, self.w[p + "attention_norm.weight"], c.norm_eps)
+        xn = self._act(rms_norm_ref(x, self.w[p + "attention_norm.weight"], c.norm_eps))
         q = self._lin(xn, p + "attention.wq.weight").reshape(-1, c.n_heads, d)
         k = self._lin(xn, p + "attention.wk.weight").reshape(-1, c.n_kv_heads, d)
         v = self._lin(xn, p + "attention.wv.weight").reshape(-1, c.n_kv_heads, d)
         cos, sin = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
-        return apply_rope_ref(q, cos, sin), apply_rope_ref(k, cos, sin), v
+        return self._act(apply_rope_ref(q, cos, sin)), self._act(apply_rope_ref(k, cos, sin)), self._act(v)
 
     def _finish_layer(self, i, x, attn):
         """wo, residual, FFN, residual (llama.py:186, 241-244, 334-338)."""
         c = self.cfg
         p = f"layers.{i}."
-        h = x + self._lin(attn.reshape(attn.shape[0], -1), p + "attention.wo.weight")
-        hn = rms_norm_ref(h, self.w[p + "ffn_norm.weight"], c.norm_eps)
-        ff = self._lin(silu_ref(self._lin(hn, p + "feed_forward.w1.weight")) * self._lin(hn, p + "feed_forward.w3.weight"),
-                       p + "feed_forward.w2.weight")
+        h = x + self._lin(self._act(attn.reshape(attn.shape[0], -1)), p + "attention.wo.weight")
+        hn = self._act(rms_norm_ref(h, self.w[p + "ffn_norm.weight"], c.norm_eps))
+        g = self._act(silu_ref(self._lin(hn, p + "feed_forward.w1.weight")) * self._lin(hn, p + "feed_forward.w3.weight"))
+        ff = self._lin(g, p + "feed_forward.w2.weight")
         return (h + ff).astype(np.float32)
 
     def _logits(self, x):
-        return self._lin(rms_norm_ref(x, self.w["norm.weight"], self.cfg.norm_eps), "output.weight")
+        return self._lin(self._act(rms_norm_ref(x, self.w["norm.weight"], self.cfg.norm_eps)), "output.weight")
 
     def _store(self, cache, slot, value, block_size):
-        if isinstance(self.cache_dtype, str) and self.cache_dtype == "bfloat16":
-            rounded = round_bf16(value)
-        else:
-            rounded = value.astype(self.cache_dtype)
+        rounded = self._round(value, self.cache_dtype)
         cache.reshape(-1, *cache.shape[2:])[slot] = rounded.astype(cache.dtype)
 
     def forward(self, tokens):

@@ -15,6 +15,9 @@
   context excludes the new slot (test_jit_decode.py:102-107), different when it
   includes it, and the cache ends up identical either way.
 * Greedy sampling: first maximum on ties (sampling.py:133-134).
+* act_dtype (16-bit activation storage, no reference counterpart): the identity
+  for float32; for bfloat16 every product input and attention operand is
+  exactly representable.
 """
 
 import numpy as np
@@ -259,6 +262,36 @@ def test_round_bf16_matches_torch():
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     truncated = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
     assert not np.array_equal(truncated, want)
+
+
+def test_act_dtype_rounds_every_product_input():
+    """act_dtype (no reference counterpart): float32 storage changes nothing,
+    bit for bit; bfloat16 storage makes the input of every product (q / k / v,
+    wo, w1 / w3, w2, the output head) and the attention operands exactly
+    bfloat16-representable, and moves the logits by a small, non-zero amount."""
+    from oracle.llama import round_bf16
+    cfg = Cfg()
+    w = rand_weights(cfg, seed=9)
+    tokens = np.random.default_rng(10).integers(0, cfg.vocab_size, 9)
+    plain = LlamaRef(cfg, w).forward(tokens)
+    assert np.array_equal(LlamaRef(cfg, w, act_dtype=np.float32).forward(tokens), plain)
+    ref = LlamaRef(cfg, w, act_dtype="bfloat16")
+    seen = []
+    lin = ref._lin
+
+    def checked_lin(x, name):
+        seen.append(name)
+        assert np.array_equal(round_bf16(x), x), name
+        return lin(x, name)
+
+    ref._lin = checked_lin
+    qkv = ref._qkv
+    ref._qkv = lambda i, x, pos: tuple(t if np.array_equal(round_bf16(t), t) else pytest.fail("q/k/v")
+                                       for t in qkv(i, x, pos))
+    got = ref.forward(tokens)
+    assert len(seen) == 7 * cfg.n_layers + 1
+    err = np.abs(got - plain).max() / max(1.0, np.abs(plain).max())
+    assert 0 < err < 5e-2
 
 
 def test_decode_attention_width_truncates_context():
