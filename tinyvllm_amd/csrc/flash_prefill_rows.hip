@@ -20,7 +20,8 @@
 //    chosen so that both the 16-row K fragment reads (ds_read_b128) and the
 //    transposing V reads (ds_read_b64_tr_b16) touch distinct banks;
 //  * four tile buffers used as two pairs: a pair of tiles (64 keys) is
-//    requested when the previous pair starts, one barrier per pair.
+//    requested when the previous pair starts, and each pair is one step (one
+//    barrier, one softmax over its 64 keys).
 // The softmax is the 64-row kernel's: log2 domain, lazy rescale (threshold 8),
 // P kept in registers as the B operand of O^T = V^T P^T; the scale is applied
 // in fp32 after the product, s * scale * log2(e) - m in one fma (llama.py:84).
@@ -36,7 +37,7 @@
 // head_dim-128 prompts.  A tile step of the longest work-group takes ~2000
 // cycles against 512 of MFMA work (clock stamps): the LDS-DMA issue, LDS read
 // issue, score wait and softmax are serial within a wave, and with 2 waves per
-// SIMD (196 VGPRs fp16, 206 bf16) little of it overlaps.  Splitting a work-group's key tiles
+// SIMD (236 VGPRs fp16, 230 bf16) little of it overlaps.  Splitting a work-group's key tiles
 // over two 4-wave groups in ping-pong (one group's MFMA phase against the
 // other's softmax phase, a barrier per phase) was correct but 2x slower: the
 // softmax phase of one wave ran ~4x longer while the other issued MFMAs.
@@ -290,21 +291,22 @@ prefill_rows_kernel(const PrefillParams pa) {
   // scores of a tile starting at key k0 -> log2 domain relative to the running
   // maximum (fp16: already, from the pre-scaled Q and the -m accumulator; bf16:
   // one fma), masked, rescaled when a row's maximum moved by more than 8
-  auto softmax = [&](f32x4 (&st)[RB][KB], int k0) {
+  auto softmax = [&](auto& st, int k0) {
+    constexpr int NKB = std::extent<std::remove_reference_t<decltype(st)>, 1>::value;   // 16-key blocks
     if constexpr (!kPreScaleQ<T>) {
 #pragma unroll
       for (int r = 0; r < RB; ++r)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) st[r][kb][i] = fmaf(st[r][kb][i], c, -mref[r]);
     }
-    if (!(k0 + BN <= klim && (!p.causal || k0 + BN - 1 <= row0))) {
+    if (!(k0 + 16 * NKB <= klim && (!p.causal || k0 + 16 * NKB - 1 <= row0))) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int rel = (p.causal ? min(klim - 1, qi[r]) : klim - 1) - (k0 + 4 * g);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) st[r][kb][i] = kb * 16 + i <= rel ? st[r][kb][i] : kNegInf;
       }
@@ -313,12 +315,11 @@ prefill_rows_kernel(const PrefillParams pa) {
     bool need_any = false;
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      // a chain of three-input maxima (v_max3_f32): the 4 KB values (an even
+      // a chain of three-input maxima (v_max3_f32): the 4 NKB values (an even
       // count) as one pair, then two more per step
-      static_assert((4 * KB) % 2 == 0, "pairs");
       float t0 = fmaxf(st[r][0][0], st[r][0][1]);
 #pragma unroll
-      for (int j = 2; j < 4 * KB; j += 2) t0 = fmaxf(t0, fmaxf(st[r][j >> 2][j & 3], st[r][(j + 1) >> 2][(j + 1) & 3]));
+      for (int j = 2; j < 4 * NKB; j += 2) t0 = fmaxf(t0, fmaxf(st[r][j >> 2][j & 3], st[r][(j + 1) >> 2][(j + 1) & 3]));
       lm[r] = t0;
       need_any = need_any || lm[r] > thr[r];
     }
@@ -334,7 +335,7 @@ prefill_rows_kernel(const PrefillParams pa) {
         for (int db = 0; db < DB; ++db) oacc[r][db] *= alpha;
         lpart[r] *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) st[r][kb] -= delta;
+        for (int kb = 0; kb < NKB; ++kb) st[r][kb] -= delta;
         mref[r] += delta;
         thr[r] = need ? 8.0f : thr[r];
         if constexpr (kPreScaleQ<T>) negm[r] = f32x4{-mref[r], -mref[r], -mref[r], -mref[r]};
@@ -343,63 +344,70 @@ prefill_rows_kernel(const PrefillParams pa) {
   };
 
   const bool idle = row0 >= p.q_len;       // rows past the prompt: nothing to compute
+  // Tiles in pairs (2s, 2s + 1), buffers 0-1 and 2-3 in turn, one step and
+  // one barrier per pair: the barrier makes every wave's loads of the pair
+  // visible and frees the previous pair's buffers, the next pair is requested
+  // into them, then the pair's 64 keys go through one softmax -- score
+  // products of both tiles, one maximum / rescale decision, P V per 32-key
+  // half.  A second tile past the last one holds a re-request of the last
+  // tile; its keys are past kend and the mask removes them.  (One barrier per
+  // tile with tiles three ahead: 58.9 / 192 / 613 us at L 2048 / 4096 / 8192,
+  // Llama-3-8B heads; a barrier per pair with a softmax per tile: 56.7 / 192 /
+  // 610; one softmax per pair: 56.1 / 191 / 600.)
   auto step = [&](auto bufc, int jj) {
     constexpr int B = decltype(bufc)::value;
-    // Tiles in pairs (2s, 2s + 1), buffers 0-1 and 2-3 in turn, one barrier
-    // per pair: at the pair's first tile this wave's loads of the pair are
-    // waited for, the barrier makes every wave's visible and frees the
-    // previous pair's buffers, and the next pair is requested into them.
-    // (One barrier per tile with tiles three ahead: 58.9 / 192 / 613 us at
-    // L 2048 / 4096 / 8192, Llama-3-8B heads, against 56.5 / 188 / 594.)
-    if constexpr (B % 2 == 0) {
-      wait_vmcnt<0>();
-      lds_barrier();
-      issue(jj + 2);
-      issue(jj + 3);
-    }
+    wait_vmcnt<0>();
+    lds_barrier();
+    issue(jj + 2);
+    issue(jj + 3);
     const int k0 = jj * BN;
-    if (idle || (p.causal && k0 > row0 + 31)) return;   // nothing visible in the tile
-    const uint8_t* sb = smem + B * BUFB;
-
-    u32x4 kf[KB][KSD];
+    if (idle || (p.causal && k0 > row0 + 31)) return;
+    f32x4 st[RB][2 * KB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint8_t* sb = smem + (B + hf) * BUFB;
+      u32x4 kf[KB][KSD];
 #pragma unroll
-      for (int ks = 0; ks < KSD; ++ks) kf[kb][ks] = *reinterpret_cast<const u32x4*>(sb + koff(ks) + kb * 16 * ROWB);
-    f32x4 st[RB][KB];
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
+        for (int ks = 0; ks < KSD; ++ks) kf[kb][ks] = *reinterpret_cast<const u32x4*>(sb + koff(ks) + kb * 16 * ROWB);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        st[r][kb] = mfma16x16x32<T>(kf[kb][0], qf[r][0], kPreScaleQ<T> ? negm[r] : f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int r = 0; r < RB; ++r)
 #pragma unroll
-        for (int ks = 1; ks < KSD; ++ks) st[r][kb] = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], st[r][kb]);
-      }
-    u32x4 vf[DB];
+        for (int kb = 0; kb < KB; ++kb) {
+          f32x4 a = mfma16x16x32<T>(kf[kb][0], qf[r][0], kPreScaleQ<T> ? negm[r] : f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(sb + voff(db)));
-      const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(sb + voff(db) + 16 * ROWB));
-      vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          for (int ks = 1; ks < KSD; ++ks) a = mfma16x16x32<T>(kf[kb][ks], qf[r][ks], a);
+          st[r][hf * KB + kb] = a;
+        }
     }
     softmax(st, k0);
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      // reduction index 8g + j: key 4g + j of block 0 (j < 4), 4g + j - 4 of block 1
-      const u32x4 pf = u32x4{pack2<T>(fast_exp2(st[r][0][0]), fast_exp2(st[r][0][1])),
-                             pack2<T>(fast_exp2(st[r][0][2]), fast_exp2(st[r][0][3])),
-                             pack2<T>(fast_exp2(st[r][1][0]), fast_exp2(st[r][1][1])),
-                             pack2<T>(fast_exp2(st[r][1][2]), fast_exp2(st[r][1][3]))};
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint8_t* sb = smem + (B + hf) * BUFB;
+      u32x4 vf[DB];
 #pragma unroll
-      for (int db = 0; db < DB; ++db) oacc[r][db] = mfma16x16x32<T>(vf[db], pf, oacc[r][db]);
-      lpart[r] = rowsum8<T>(pf, lpart[r]);
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(sb + voff(db)));
+        const u32x2 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(sb + voff(db) + 16 * ROWB));
+        vf[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        // reduction index 8g + j: key 4g + j of the half's first 16-key block
+        // (j < 4), 4g + j - 4 of its second
+        const f32x4 s0 = st[r][hf * KB], s1 = st[r][hf * KB + 1];
+        const u32x4 pf = u32x4{pack2<T>(fast_exp2(s0[0]), fast_exp2(s0[1])), pack2<T>(fast_exp2(s0[2]), fast_exp2(s0[3])),
+                               pack2<T>(fast_exp2(s1[0]), fast_exp2(s1[1])), pack2<T>(fast_exp2(s1[2]), fast_exp2(s1[3]))};
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[r][db] = mfma16x16x32<T>(vf[db], pf, oacc[r][db]);
+        lpart[r] = rowsum8<T>(pf, lpart[r]);
+      }
     }
   };
   for (int jj = 0; jj < ntiles; jj += NB) {    // unrolled over the buffers: LDS offsets are constants
     step(std::integral_constant<int, 0>{}, jj);
-    if (jj + 1 < ntiles) step(std::integral_constant<int, 1>{}, jj + 1);
     if (jj + 2 < ntiles) step(std::integral_constant<int, 2>{}, jj + 2);
-    if (jj + 3 < ntiles) step(std::integral_constant<int, 3>{}, jj + 3);
   }
   wait_vmcnt<0>();               // the clamped trailing loads land before the work-group ends
 
