@@ -30,8 +30,8 @@
 // query at the end.
 //
 // Measured on MI355X (Llama-3-8B heads, Hq 32 / Hkv 8, head_dim 128, fp16,
-// causal): L 2048 58 us (53-54 us replayed in a graph) against 64-68 for the
-// 64-row kernel, L 4096 ~195 against 207-210; at L <= 1024 and at head_dim 64
+// causal): L 2048 54-56 us (51 us replayed in a graph) against 64-68 for the
+// 64-row kernel, L 4096 184-191 against 207-210; at L <= 1024 and at head_dim 64
 // the 64-row kernel is faster (L 512 / 1024 at head_dim 64: 7.6 / 13.0 us
 // against 12.1 / 20.7), so the launcher uses this one only for long
 // head_dim-128 prompts.  A tile step of the longest work-group takes ~2000
