@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from oracle.kv_cache import reshape_and_cache_ref
+from tests.random_cases import case_count, case_seed
 
 pytestmark = pytest.mark.gpu
 
@@ -149,6 +150,50 @@ def test_fused_write_strided_rows_and_error_count():
     for i, s in enumerate([0, 9, 31]):
         assert torch.equal(flat_k[s], k[i]) and torch.equal(flat_v[s], v[i])
     assert flat_k.abs().sum(dim=(1, 2)).nonzero().flatten().tolist() == [0, 9, 31]
+
+
+def _random_write_cases(n=None, seed=91):
+    n = case_count(8) if n is None else n
+    rng = np.random.Generator(np.random.PCG64(case_seed(seed)))
+    cases = []
+    for i in range(n):
+        nb = int(rng.integers(1, 200))
+        bs = int(rng.choice([1, 4, 8, 12, 16, 32]))
+        hkv = int(rng.choice([1, 2, 3, 4, 8]))
+        d = int(rng.choice([2, 8, 32, 64, 80, 128, 256]))
+        t = int(rng.integers(1, min(600, nb * bs) + 1))
+        dtype = [torch.float32, torch.float16, torch.bfloat16][int(rng.integers(0, 3))]
+        cases.append((i, nb, bs, hkv, d, t, dtype))
+    return cases
+
+
+@pytest.mark.parametrize("i,nb,bs,hkv,d,t,dtype", _random_write_cases())
+def test_random_fused_writes(i, nb, bs, hkv, d, t, dtype):
+    """Seeded random pools (1-199 blocks of 1-32 rows), head shapes, token
+    counts and dtypes; slots a random injective map with padding (-1) and
+    out-of-range entries mixed in: the cache equals the oracle placement bit
+    for bit, out-of-range slots are skipped and counted."""
+    from tinyvllm_amd.kv_cache import reshape_and_cache
+    rng = np.random.Generator(np.random.PCG64(case_seed(700 + i)))
+    slots = rng.permutation(nb * bs)[:t].astype(np.int32)
+    kind = rng.integers(0, 10, t)
+    slots[kind == 0] = -1                                          # padding tokens
+    bad = kind == 1
+    slots[bad] = nb * bs + rng.integers(0, 1000, int(bad.sum()))   # past the cache
+    k = torch.from_numpy(rng.standard_normal((t, hkv, d), dtype=np.float32)).to(dtype)
+    v = torch.from_numpy(rng.standard_normal((t, hkv, d), dtype=np.float32)).to(dtype)
+    kc = torch.from_numpy(rng.standard_normal((nb, bs, hkv, d), dtype=np.float32)).to(dtype)
+    vc = torch.from_numpy(rng.standard_normal((nb, bs, hkv, d), dtype=np.float32)).to(dtype)
+    ib = torch.int16 if dtype != torch.float32 else torch.int32
+    kc_bits, vc_bits = kc.view(ib).numpy().copy(), vc.view(ib).numpy().copy()
+    kg, vg = kc.cuda(), vc.cuda()
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    reshape_and_cache(kg, vg, k.cuda(), v.cuda(), torch.from_numpy(slots).cuda(), err_count=err)
+    keep = np.where(bad, -1, slots).astype(np.int32)
+    reshape_and_cache_ref(kc_bits, vc_bits, k.view(ib).numpy(), v.view(ib).numpy(), keep)
+    assert err.item() == int(bad.sum())
+    assert np.array_equal(kg.cpu().view(ib).numpy(), kc_bits)
+    assert np.array_equal(vg.cpu().view(ib).numpy(), vc_bits)
 
 
 def test_prefill_slot_mapping_drives_fused_write():
