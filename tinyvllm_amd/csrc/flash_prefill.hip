@@ -697,7 +697,7 @@ void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) 
 // 128-row work-groups with LDS-DMA tiles (prefill_rows_kernel,
 // flash_prefill_rows.hip) for long head_dim-128 prompts, where they measured
 // faster (MI355X, Hq 32 / Hkv 8: L 2048 54-56 against 64-68 us, L 4096
-// 184-191 against 207-210); below 2048 rows, or at head_dim 64, this file's 64-row
+// 174 against 207-210); below 2048 rows, or at head_dim 64, this file's 64-row
 // kernel wins.
 #ifndef TV_PREFILL_ROWS_MODE
 #define TV_PREFILL_ROWS_MODE 1     // 0: never, 1: long head_dim-128 prompts, 2: always (when the shape allows)

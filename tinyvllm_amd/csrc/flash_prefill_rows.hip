@@ -31,7 +31,7 @@
 //
 // Measured on MI355X (Llama-3-8B heads, Hq 32 / Hkv 8, head_dim 128, fp16,
 // causal): L 2048 54-56 us (51 us replayed in a graph) against 64-68 for the
-// 64-row kernel, L 4096 184-191 against 207-210; at L <= 1024 and at head_dim 64
+// 64-row kernel, L 4096 174 against 207-210; at L <= 1024 and at head_dim 64
 // the 64-row kernel is faster (L 512 / 1024 at head_dim 64: 7.6 / 13.0 us
 // against 12.1 / 20.7), so the launcher uses this one only for long
 // head_dim-128 prompts.  A tile step of the longest work-group takes ~2000
@@ -134,9 +134,16 @@ template <typename T> __device__ __forceinline__ float rowsum8(u32x4 p, float ac
 
 }  // namespace
 
-// Query tile of unit u, zig-zag: the longer half of the causal tiles longest
-// first, then the shorter half shortest first.
-__device__ __forceinline__ int rows_unit_tile(int u, int nqt) {
+// Query tile of unit u.  Grids whose work-groups are all resident at once:
+// zig-zag, the longer half of the causal tiles longest first, then the shorter
+// half shortest first (dispatched a slot per CU at a time, so a CU's two
+// work-groups hold a long and a short tile).  Larger grids: longest first, so
+// the last work-groups to start are the shortest (MI355X, Llama-3-8B heads,
+// fp16: L 2048 54.6 us zig-zag against 58.1 longest first; L 4096 174 against
+// 188-191 and L 8192 562 against 598 longest first against zig-zag; ascending
+// and alternating orders were slower at every length).
+__device__ __forceinline__ int rows_unit_tile(int u, int nqt, bool longest_first) {
+  if (longest_first) return nqt - 1 - u;
   const int half = (nqt + 1) / 2;
   return u < half ? nqt - 1 - u : u - half;
 }
@@ -177,7 +184,7 @@ prefill_rows_kernel(const PrefillParams pa) {
 
   const int h = p.xcd_remap ? ((int)(blockIdx.x & 7) * (p.num_heads >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
   const int nqt = (p.q_len + BM - 1) / BM;
-  const int qt = rows_unit_tile(blockIdx.y, nqt);
+  const int qt = rows_unit_tile(blockIdx.y, nqt, p.longest_first != 0);
   const int kvh = h / (p.num_heads / p.num_kv_heads);
   const int klim = p.kv_len;
   const int kend = p.causal ? min(klim, (qt + 1) * BM) : klim;
@@ -430,17 +437,42 @@ prefill_rows_kernel(const PrefillParams pa) {
   }
 }
 
+// Work-groups of prefill_rows_kernel<T, D> resident at once on the current
+// device (occupancy x CUs), queried once per device.
+template <typename T, int D>
+long long rows_resident() {
+  static long long cache[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cache[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prefill_rows_kernel<T, D>, 256, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    cache[dev] = (long long)per_cu * cus;
+  }
+  return cache[dev];
+}
+
+template <typename T, int D>
+void launch_rows(const PrefillParams& pp_in, int num_seqs, int max_q_len, hipStream_t stream) {
+  const dim3 grid(pp_in.num_heads, (max_q_len + kRowsBM - 1) / kRowsBM, num_seqs);
+  PrefillParams pp = pp_in;
+  pp.longest_first = (long long)grid.x * grid.y * grid.z > rows_resident<T, D>() ? 1 : 0;
+  hipLaunchKernelGGL((prefill_rows_kernel<T, D>), grid, dim3(256), 0, stream, pp);
+}
+
 // Launch for one prompt (grid.z = 1) or several (cu_q set; grid.z = prompts).
 // Returns false when the shape is not handled here.
 bool launch_prefill_rows(const PrefillParams& pp, int dtype, int num_seqs, int max_q_len, hipStream_t stream) {
   if (!(dtype == kF16 || dtype == kBF16) || !(pp.head_dim == 64 || pp.head_dim == 128)) return false;
-  const dim3 grid(pp.num_heads, (max_q_len + kRowsBM - 1) / kRowsBM, num_seqs);
   if (dtype == kF16) {
-    if (pp.head_dim == 64) hipLaunchKernelGGL((prefill_rows_kernel<_Float16, 64>), grid, dim3(256), 0, stream, pp);
-    else hipLaunchKernelGGL((prefill_rows_kernel<_Float16, 128>), grid, dim3(256), 0, stream, pp);
+    if (pp.head_dim == 64) launch_rows<_Float16, 64>(pp, num_seqs, max_q_len, stream);
+    else launch_rows<_Float16, 128>(pp, num_seqs, max_q_len, stream);
   } else {
-    if (pp.head_dim == 64) hipLaunchKernelGGL((prefill_rows_kernel<__bf16, 64>), grid, dim3(256), 0, stream, pp);
-    else hipLaunchKernelGGL((prefill_rows_kernel<__bf16, 128>), grid, dim3(256), 0, stream, pp);
+    if (pp.head_dim == 64) launch_rows<__bf16, 64>(pp, num_seqs, max_q_len, stream);
+    else launch_rows<__bf16, 128>(pp, num_seqs, max_q_len, stream);
   }
   return true;
 }

@@ -46,6 +46,9 @@ struct PrefillParams {
   // (0: top-left aligned, the reference's prompt; start_pos: a chunk after a
   // cached prefix).
   int q_pos_offset;
+  // 128-row kernel: 1 deals query tiles longest first (grids with more
+  // work-groups than are resident at once), 0 zig-zag (prefill_rows_kernel).
+  int longest_first;
 };
 
 // Cache write from a slot mapping or a base slot (kv_cache.hip).
