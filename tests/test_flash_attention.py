@@ -139,6 +139,50 @@ def test_long_prompts_head_dim_128(dtype, causal, lq, lk, scale):
     check(q.to(dtype), k.to(dtype), v.to(dtype), causal)
 
 
+def _check_heads(out, q, k, v, causal, groups, dtype):
+    """Oracle rows of the query heads of the listed KV groups only (the float64
+    oracle over every head of a large grid would take minutes)."""
+    hq, hkv = q.shape[1], k.shape[1]
+    g = hq // hkv
+    for kvh in groups:
+        hs = slice(kvh * g, (kvh + 1) * g)
+        want = flash_prefill_ref(q[:, hs].float().numpy()[None], k[:, kvh:kvh + 1].float().numpy()[None],
+                                 v[:, kvh:kvh + 1].float().numpy()[None], causal)[0]
+        err = np.abs(out[:, hs].float().cpu().numpy() - want).max()
+        assert err <= TOL[dtype], (kvh, err)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_long_prompt_grid_larger_than_resident(dtype, causal):
+    """Hq 48 / Hkv 8 at L 2100: 816 work-groups of the 128-row kernel, more
+    than are resident at once, so query tiles are dealt longest first (an odd
+    tile count and a partial last tile); rows of two KV groups' query heads
+    against the oracle -- the tile order is the same for every head."""
+    lq = 2100
+    q = randn(140, lq, 48, 128).to(dtype)
+    k = randn(141, lq, 8, 128).to(dtype)
+    v = randn(142, lq, 8, 128).to(dtype)
+    out = flash(q, k, v, causal)
+    _check_heads(out, q, k, v, causal, [0, 7], dtype)
+
+
+def test_varlen_long_prompts_grid_larger_than_resident():
+    """Two long prompts packed (Hq 32: grid 32 x 18 x 2 = 1152 work-groups of
+    the 128-row kernel, longest-first tiles within each prompt)."""
+    from tinyvllm_amd.attention import flash_prefill_varlen
+    lens = [2300, 2048]
+    tot = sum(lens)
+    q, k, v = (randn(143 + i, tot, 32 if i == 0 else 8, 128, dtype=torch.float16) for i in range(3))
+    out = flash_prefill_varlen(q.cuda(), k.cuda(), v.cuda(), lens, True)
+    torch.cuda.synchronize()
+    s = 0
+    for n in lens:
+        sl = slice(s, s + n)
+        _check_heads(out[sl], q[sl], k[sl], v[sl], True, [0, 5], torch.float16)
+        s += n
+
+
 @pytest.mark.parametrize("length", [512, 1024])
 def test_tinyllama_prefill_shape(length):
     """TinyLlama prefill shape: Hq 32, Hkv 4, D 64, fp16 inputs, causal."""
