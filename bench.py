@@ -266,14 +266,23 @@ def bench_prefill(steps, warmup):
     wms = timed(write, steps, warmup, graph=True)
     tot = sum(per)
     flops = wl.flops()
-    # Llama-3-8B heads (Hq 32 / Hkv 8, head_dim 128), one 2048-token prompt.
-    g = torch.Generator(device="cuda").manual_seed(0)
-    L8, hq8, hkv8, d8 = 2048, 32, 8, 128
-    q8 = torch.randn((1, L8, hq8, d8), generator=g, device="cuda").half()
-    k8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
-    v8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
-    ms8 = timed(PrefillPlan(q8, k8, v8, True).run, steps, warmup, graph=True)
-    flops8 = 2 * hq8 * d8 * L8 * (L8 + 1)
+    # Llama-3-8B heads (Hq 32 / Hkv 8, head_dim 128), one prompt of 2048, 4096
+    # and 8192 tokens (the 128-row kernel; at 4096+ the grid holds more
+    # work-groups than are resident at once).
+    long_prompts = {}
+    for L8 in (2048, 4096, 8192):
+        g = torch.Generator(device="cuda").manual_seed(0)
+        hq8, hkv8, d8 = 32, 8, 128
+        q8 = torch.randn((1, L8, hq8, d8), generator=g, device="cuda").half()
+        k8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
+        v8 = torch.randn((1, L8, hkv8, d8), generator=g, device="cuda").half()
+        ms8 = timed(PrefillPlan(q8, k8, v8, True).run, steps, warmup, graph=True)
+        flops8 = 2 * hq8 * d8 * L8 * (L8 + 1)
+        long_prompts[f"llama3_8b_heads_f16_L{L8}"] = {
+            "value": round(flops8 / (ms8 * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+            "ms": round(ms8, 5), "flops": flops8,
+            "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)}
+        del q8, k8, v8
     chunk = bench_chunk_over_prefix(steps, warmup)
     return wl, {
         "workload": "prefill_tinyllama_f16_L512+L1024 (Hq32 Hkv4 D64, causal) + fused KV write",
@@ -285,10 +294,7 @@ def bench_prefill(steps, warmup):
                        "ms": round(ms_packed, 5), "note": "both prompts in one tv_flash_prefill_varlen launch"},
         "kv_write_ms": round(wms, 5),
         "kv_write_gbs": round(wl.kv_write_bytes() / (wms * 1e-3) / 1e9, 1),
-        "llama3_8b_heads_f16_L2048": {
-            "value": round(flops8 / (ms8 * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
-            "ms": round(ms8, 5), "flops": flops8,
-            "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)},
+        **long_prompts,
         "chunk_over_cached_prefix": chunk,
     }
 
@@ -517,7 +523,7 @@ def main():
             cb["us_per_call"] = round(cb["ms_per_call"] * 1e3, 1)
             configs["decode_tinyllama_f32_b4"]["cpu_baseline"] = cb
         del wl1
-        log("bench: causal prefill TinyLlama shape L512 + L1024 (and Llama-3-8B heads L2048)")
+        log("bench: causal prefill TinyLlama shape L512 + L1024 (and Llama-3-8B heads L2048 / 4096 / 8192)")
         wl2, configs["prefill_tinyllama_f16"] = bench_prefill(args.steps, args.warmup)
         if cpu_on:
             configs["prefill_tinyllama_f16"]["cpu_baseline"] = cpu_baseline_prefill(wl2, env=env)
