@@ -225,6 +225,36 @@ def cpu_baseline_e2e(state, env=None):
     want = ref.decode(first, [L] * B, [L + 1] * B, tables, kc, vc, kv.block_size)
     el = time.perf_counter() - t0
     got = state["step1_logits"]
+    # teacher-forced: the oracle decodes every step of the run on the device's
+    # tokens and K/V rows for the kept sequences (llama.py:346-388,
+    # sampling.py:131-134); logits within 2e-2, greedy token equal where the
+    # oracle's top two logits are more than 2 x 2e-2 apart
+    seqs, steps = state["tf_seqs"], state["steps"]
+    ncols = -(-(L + steps) // kv.block_size)
+    ids = torch.from_numpy(wl.tables[seqs, :ncols].reshape(-1).astype(np.int64)).cuda()
+    tkc = [k.index_select(0, ids).float().cpu().numpy() for k in kv.k_cache]
+    tvc = [v.index_select(0, ids).float().cpu().numpy() for v in kv.v_cache]
+    ttab = np.arange(len(seqs) * ncols, dtype=np.int32).reshape(len(seqs), ncols)
+    n = len(seqs)
+    worst, matches, clear_total, clear_match = 0.0, [], 0, 0
+    t1 = time.perf_counter()
+    for i in range(steps):
+        want_i = ref.decode([int(t) for t in state["tf_inputs"][i]], [L + i] * n, [L + i + 1] * n, ttab, tkc, tvc,
+                            kv.block_size)
+        got_i = state["tf_logits"][i]
+        worst = max(worst, float(np.abs(got_i - want_i).max()))
+        top2 = np.sort(want_i, axis=1)[:, -2:]
+        clear = top2[:, 1] - top2[:, 0] > 2 * 2e-2
+        gt = np.argmax(got_i, 1)
+        clear_total += int(clear.sum())
+        clear_match += int((gt[clear] == greedy_ref(want_i)[clear]).sum())
+        matches += (gt == greedy_ref(want_i)).tolist()
+    state["tf_parity"] = {"sequences": seqs, "steps": steps, "logits_max_abs": round(worst, 6),
+                          "token_match_rate_128": round(float(np.mean(matches)), 4),
+                          "clear_margin_matches": f"{clear_match}/{clear_total}",
+                          "clear_margin_match_rate": round(clear_match / max(1, clear_total), 4),
+                          "tolerance": 2e-2, "clear_margin": 4e-2,
+                          "seconds": round(time.perf_counter() - t1, 1)}
     return _cpu_entry(round(B / el, 3), "tok/s",
                       f"one step at batch {B}, context {L} (the GPU's step 1, K/V gathered from the device), "
                       f"numpy float32 restatement of llama.py:290-388; tok/s = {B} / step time "
@@ -234,14 +264,37 @@ def cpu_baseline_e2e(state, env=None):
                               "step1_greedy_match_rate": round(float(np.mean(np.argmax(got, 1) == greedy_ref(want))), 4),
                               "tolerance": 2e-2, "sequences": B})
 
-def bench_decode(wl, steps, warmup, graph):
+def per_launch_ms(fn, launches):
+    """Each of ``launches`` calls of ``fn`` timed alone (HIP events around one
+    launch on the launch stream, the previous one finished): (median, min, max) ms."""
+    import torch
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in ev)
+    return t[len(t) // 2], t[0], t[-1]
+
+
+def bench_decode(wl, steps, warmup, graph, per_launch=0):
     from tinyvllm_amd.attention import PagedDecodePlan
     plan = PagedDecodePlan(wl.q, wl.k_cache, wl.v_cache, wl.bt_dev, wl.ctx_dev, wl.num_heads,
                            wl.num_kv_heads, wl.head_dim, wl.block_size)
     ms = timed(plan.run, steps, warmup, graph)
     gbs = wl.algorithmic_bytes() / (ms * 1e-3) / 1e9
-    return {"ms": ms, "gbs": gbs, "bytes": wl.algorithmic_bytes(), "flops": wl.flops(),
-            "partition_size": plan.partition_size}
+    out = {"ms": ms, "gbs": gbs, "bytes": wl.algorithmic_bytes(), "flops": wl.flops(),
+           "partition_size": plan.partition_size}
+    if per_launch:
+        med, lo, hi = per_launch_ms(plan.run, per_launch)
+        out["per_launch"] = {"launches": per_launch, "median_ms": round(med, 5), "min_ms": round(lo, 5),
+                             "max_ms": round(hi, 5),
+                             "median_gbs": round(wl.algorithmic_bytes() / (med * 1e-3) / 1e9, 1),
+                             "median_frac_of_hbm_peak": round(wl.algorithmic_bytes() / (med * 1e-3) / 1e9
+                                                              / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def bench_prefill(steps, warmup):
@@ -432,13 +485,30 @@ def bench_e2e(decode_steps=128, warmup=3):
     hist = g.history[:, L + 1:L + 1 + decode_steps].cpu().numpy().astype(np.int64)
     nbytes = wl.bytes_for_steps(L, decode_steps)
     g.close()
+    # the same steps driven from the host (tokens copied in every step), keeping
+    # the logits of two sequences for the CPU leg's teacher-forced parity check
+    # over the whole run; their tokens must equal the timed device loop's
+    tf_seqs = [0, B - 1]
+    sel = torch.tensor(tf_seqs, device="cuda")
+    hg = DecodeGraph(m, kv, B, wl.tables.shape[1])
+    cur = first.clone()
+    tf_inputs, tf_logits, host_equal = [], [], True
+    for i in range(decode_steps):
+        tf_inputs.append(cur.cpu().numpy()[tf_seqs])
+        hg.set_inputs(cur, [L + i] * B, [L + i + 1] * B, wl.tables)
+        hg.step()
+        cur = hg.tokens.clone()
+        tf_logits.append(hg.logits.index_select(0, sel).cpu().numpy())
+        host_equal &= bool(np.array_equal(cur.cpu().numpy(), hist[:, i]))
+    hg.close()
     # step 1 again from the prefilled state, keeping its logits for the parity
-    # check of the CPU leg (rows written by the timed steps past position L are
-    # never attended by step 1)
+    # check of the CPU leg (rows written past position L are never attended by
+    # step 1)
     g1 = DecodeGraph(m, kv, B, wl.tables.shape[1])
     g1.set_inputs(first, [L] * B, [L + 1] * B, wl.tables)
     g1.step()
-    state = {"wl": wl, "first": first.cpu().numpy(), "step1_logits": g1.logits.cpu().numpy()}
+    state = {"wl": wl, "first": first.cpu().numpy(), "step1_logits": g1.logits.cpu().numpy(),
+             "tf_seqs": tf_seqs, "tf_inputs": tf_inputs, "tf_logits": tf_logits, "steps": decode_steps}
     g1.close()
     return state, {
         "workload": "tinyllama_1.1b_random_init_f16 decode: B64, prompts 1024 (seeded), 128 greedy steps, "
@@ -456,6 +526,7 @@ def bench_e2e(decode_steps=128, warmup=3):
         "prefill_ms": round(prefill_ms, 2),
         "tokens_checksum": int((hist * (np.arange(hist.size).reshape(hist.shape) % 9973 + 1)).sum()),
         "first_tokens_seq0": hist[0, :8].tolist(),
+        "host_driven_steps_equal_device_loop": host_equal,
     }
 
 
@@ -507,7 +578,7 @@ def main():
     log("bench: paged decode B256 Hq32 Hkv8 D128 fp16")
     wl3 = workloads.decode_llama3_8b_b256()
     torch.cuda.synchronize()
-    r3 = bench_decode(wl3, args.steps, args.warmup, graph=False)
+    r3 = bench_decode(wl3, args.steps, args.warmup, graph=False, per_launch=64)
     log(f"bench: paged decode B256 {r3['ms']:.4f} ms {r3['gbs']:.1f} GB/s")
 
     configs = {}
@@ -537,6 +608,7 @@ def main():
         if cpu_on:
             log("bench: TinyLlama decode cpu baseline (one oracle step at B64)")
             configs["e2e_tinyllama_decode"]["cpu_baseline"] = cpu_baseline_e2e(state, env=env)
+            configs["e2e_tinyllama_decode"]["parity"] = state["tf_parity"]
         del state
         torch.cuda.empty_cache()
         log("bench: streaming-read ceiling (2 GiB)")
@@ -576,6 +648,7 @@ def main():
                      "traffic_source": PRIMARY_TRAFFIC_SOURCE,
                      "algorithmic_bytes_per_launch": r3["bytes"],
                      "timing": "HIP events over K launches of decode+merge on the launch stream"},
+        "per_launch": r3["per_launch"],
         "frac_of_read_ceiling": (round(r3["gbs"] / configs["hbm_read_ceiling"]["value"], 4)
                                  if "hbm_read_ceiling" in configs else None),
         "cpu_baseline": cpu,

@@ -106,7 +106,8 @@ int tv_paged_decode(void* out, const void* queries, const void* k_cache, const v
  * that forbid hipMalloc).  Arguments and results are those of tv_paged_decode
  * with workspace = that scratch.  A launch whose tv_paged_decode_workspace_bytes
  * exceeds 16 MiB fails with TV_EINVAL.  Allocates nothing; the first call on a
- * device looks the scratch address up once.  All calls on one device share the
+ * device looks the scratch address up once, so make that call eagerly before
+ * capturing later calls into a graph.  All calls on one device share the
  * scratch: calls that overlap on one device (different streams, or host
  * threads) race and must be serialised by the caller.
  */

@@ -151,3 +151,80 @@ def test_prepare_batch_tensors_matches_engine(max_blocks):
     assert np.array_equal(pad_or_truncate_ref(bt, max_blocks), bt)
     wider = pad_or_truncate_ref(bt, max_blocks + 3)
     assert wider.shape == (5, max_blocks + 3) and not wider[:, max_blocks:].any()
+
+
+def _literal_script(cls):
+    """10 blocks of 4 tokens, LIFO from list(range(10)) (block_manager.py:13-15,
+    37): sequence 0 holds 6 tokens, 1 holds 1, 2 holds 13, 3 is registered
+    with none."""
+    bm = cls(1, 10, 4)
+    for sid, n in enumerate([6, 1, 13, 0]):
+        bm.register_sequence(sid)
+        if n:
+            bm.ensure_block_for_position(sid, n - 1)
+    return bm
+
+
+# Hand-enumerated from the reference's rules, not from either implementation:
+# tables 0: [9, 8], 1: [7], 2: [6, 5, 4, 3], 3: []; rows zero-padded or
+# truncated to max_blocks (engine.py:246-250); ctx = start + 1 (engine.py:251).
+LITERAL_STARTS = [5, 0, 12, 0]
+LITERAL_CTX = [6, 1, 13, 1]
+LITERAL_BT = {
+    3: [[9, 8, 0], [7, 0, 0], [6, 5, 4], [0, 0, 0]],                                 # sequence 2 truncated
+    5: [[9, 8, 0, 0, 0], [7, 0, 0, 0, 0], [6, 5, 4, 3, 0], [0, 0, 0, 0, 0]],
+    1: [[9], [7], [6], [0]],
+}
+
+
+@pytest.mark.parametrize("max_blocks", sorted(LITERAL_BT))
+def test_prepare_batch_tensors_hand_enumerated(max_blocks):
+    for cls in (BlockManager, BlockManagerRef):
+        bm = _literal_script(cls)
+        assert [bm.get_block_table(s) for s in range(4)] == [[9, 8], [7], [6, 5, 4, 3], []]
+        if cls is BlockManager:
+            bt, ctx = bm.prepare_batch_tensors([0, 1, 2, 3], LITERAL_STARTS, max_blocks)
+        else:
+            bt, ctx = prepare_batch_tensors_ref(bm, [0, 1, 2, 3], LITERAL_STARTS, max_blocks)
+        assert bt.dtype == np.int32 and ctx.dtype == np.int32
+        assert bt.tolist() == LITERAL_BT[max_blocks], cls
+        assert ctx.tolist() == LITERAL_CTX, cls
+
+
+def test_pad_or_truncate_hand_enumerated():
+    # Llama.decode's pad / truncate to the JIT width (llama.py:368-374)
+    bt = np.array(LITERAL_BT[5], np.int32)
+    assert pad_or_truncate_ref(bt, 2).tolist() == [[9, 8], [7, 0], [6, 5], [0, 0]]
+    assert pad_or_truncate_ref(bt, 7).tolist() == [[9, 8, 0, 0, 0, 0, 0], [7, 0, 0, 0, 0, 0, 0],
+                                                   [6, 5, 4, 3, 0, 0, 0], [0, 0, 0, 0, 0, 0, 0]]
+    assert pad_or_truncate_ref(bt, 5).tolist() == LITERAL_BT[5]
+
+
+def test_slot_mapping_hand_enumerated():
+    """slot = block_id * block_size + position % block_size (llama.py:199-209),
+    worked out by hand for 6 blocks of 4 tokens, LIFO: a 6-token prompt takes
+    blocks 5, 4; a 3-token prompt block 3; decode then writes position 6 of the
+    first sequence at block 4 offset 2, and its position 8 opens block 2."""
+    for cls in (BlockManager, BlockManagerRef):
+        bm = cls(1, 6, 4)
+        bm.register_sequence(0)
+        bm.register_sequence(1)
+        if cls is BlockManager:
+            s0 = bm.prefill_slot_mapping(0, 0, 6).tolist()
+            s1 = bm.prefill_slot_mapping(1, 0, 3).tolist()
+        else:
+            s0 = slots_from_plan(write_kv_plan_ref(bm, 0, 0, 6, 0), 4)   # layer 0, sequence 0, 6 tokens from 0
+            s1 = slots_from_plan(write_kv_plan_ref(bm, 0, 1, 3, 0), 4)
+        assert list(s0) == [20, 21, 22, 23, 16, 17], cls
+        assert list(s1) == [12, 13, 14], cls
+        for _ in range(6):
+            bm.advance_position(0)
+        for _ in range(3):
+            bm.advance_position(1)
+        _, blk, off = bm.get_slot(0)
+        assert (blk, off) == (4, 2)
+        bm.advance_position(0)
+        bm.advance_position(0)
+        _, blk, off = bm.get_slot(0)                      # position 8: a new block, popped LIFO
+        assert (blk, off) == (2, 0)
+        assert bm.get_block_table(0) == [5, 4, 2]

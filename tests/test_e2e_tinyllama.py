@@ -13,12 +13,15 @@ device wrote (gathered into a compact cache for the checked sequences):
 * one 1024-token prompt through the oracle's prefill: last-position logits
   within 2e-2 and sampled cache rows of every layer;
 * step-1 logits of 4 sequences (first, last and two seeded picks) within 2e-2;
-* 128 device-side steps: the first 8 equal 8 host-driven steps bit for bit,
-  and 2 sequences teacher-forced through the oracle for 8 steps keep their
-  logits within 2e-2; the greedy token must match wherever the oracle's top two
-  logits are more than 2 x 2e-2 apart (near ties may flip either way), and the
-  raw match rate is printed.
+* 128 device-side steps equal 128 host-driven steps bit for bit (tokens of all
+  64 sequences at every step), and 4 sequences (first, last and two seeded
+  picks) teacher-forced through the oracle for all 128 steps keep their logits
+  within 2e-2 at every step; the greedy token must match wherever the
+  oracle's top two logits are more than 2 x 2e-2 apart (near ties may flip
+  either way), and the raw match rate is printed.
 """
+
+import time
 
 import numpy as np
 import pytest
@@ -121,7 +124,7 @@ def test_128_device_steps_equal_host_steps_and_oracle(e2e):
     from tinyvllm_amd.llama import DecodeGraph
     wl, first, ref = e2e
     m, kv = wl.model, wl.kv
-    B, L, steps, check = wl.batch, wl.prompt_len, wl.decode_steps, 8
+    B, L, steps = wl.batch, wl.prompt_len, wl.decode_steps
     g = DecodeGraph(m, kv, B, wl.tables.shape[1], keep_logits=False, history_len=L + steps + 2)
     g.set_inputs(first, [L] * B, [L + 1] * B, wl.tables)
     g.run(steps)
@@ -132,31 +135,41 @@ def test_128_device_steps_equal_host_steps_and_oracle(e2e):
     g.close()
     _say(f"e2e: {steps} device steps done")
     # host-driven steps (tokens copied in every step) reproduce the device loop
+    # at every one of the 128 steps; the logits of the checked sequences are kept
+    seqs = sorted({0, B - 1, *np.random.Generator(np.random.PCG64(5)).choice(np.arange(1, B - 1), 2,
+                                                                              replace=False).tolist()})
+    sel = torch.tensor(seqs, device="cuda")
     h = DecodeGraph(m, kv, B, wl.tables.shape[1])
     cur = first.clone()
     inputs, step_logits = [], []
-    for i in range(check):
-        inputs.append(cur.cpu().numpy())
+    for i in range(steps):
+        inputs.append(cur.cpu().numpy()[seqs])
         h.set_inputs(cur, [L + i] * B, [L + i + 1] * B, wl.tables)
         h.step()
         cur = h.tokens.clone()
-        step_logits.append(h.logits.cpu().numpy())
+        step_logits.append(h.logits.index_select(0, sel).cpu().numpy())
         assert np.array_equal(cur.cpu().numpy(), hist[:, L + 1 + i]), i
     h.close()
-    # teacher-forced oracle over the device's own tokens and K/V rows
-    seqs = [3, 40]
-    kc, vc, tables = compact_cache(wl, seqs, (L + check) // 16 + 1)
-    matches, clear_ok = [], True
-    for i in range(check):
-        toks = [int(inputs[i][b]) for b in seqs]
-        want = ref.decode(toks, [L + i] * 2, [L + i + 1] * 2, tables, kc, vc, 16)
-        got = step_logits[i][seqs]
+    _say(f"e2e: {steps} host-driven steps equal the device loop")
+    # the oracle teacher-forced over all 128 steps on the device's own tokens and
+    # K/V rows: logits within 2e-2 at every step, the greedy token equal wherever
+    # the oracle's top two logits are more than 2 x 2e-2 apart
+    kc, vc, tables = compact_cache(wl, seqs, -(-(L + steps) // 16))      # blocks of positions 0 .. L + steps - 1
+    n = len(seqs)
+    matches, clear_total, clear_match, worst = [], 0, 0, 0.0
+    t0 = time.perf_counter()
+    for i in range(steps):
+        want = ref.decode([int(t) for t in inputs[i]], [L + i] * n, [L + i + 1] * n, tables, kc, vc, 16)
+        got = step_logits[i]
         err = float(np.abs(got - want).max())
+        worst = max(worst, err)
         assert err <= TOL, f"step {i}: max-abs {err}"
         top2 = np.sort(want, axis=1)[:, -2:]
         clear = top2[:, 1] - top2[:, 0] > 2 * TOL
         gt = np.argmax(got, 1)
-        clear_ok &= bool(np.array_equal(gt[clear], greedy_ref(want)[clear]))
+        clear_total += int(clear.sum())
+        clear_match += int((gt[clear] == greedy_ref(want)[clear]).sum())
         matches += (gt == greedy_ref(want)).tolist()
-    _say(f"e2e teacher-forced sequences {seqs} x {check} steps: greedy match rate {np.mean(matches):.3f}")
-    assert clear_ok
+    _say(f"e2e teacher-forced sequences {seqs} x {steps} steps ({time.perf_counter() - t0:.1f} s): logits max-abs "
+         f"{worst:.3e}, greedy match rate {np.mean(matches):.4f}, clear-margin {clear_match}/{clear_total}")
+    assert clear_match == clear_total

@@ -469,13 +469,19 @@ def test_random_paged_prefill(i, dtype, d, hq, hkv, start, n, bs, causal):
     test_paged_prefill_equals_last_rows_of_whole_prompt(dtype, d, hq, hkv, start, n, bs, causal)
 
 
-def test_paged_prefill_invalid_block_id_gives_nan():
+@pytest.mark.parametrize("dtype,out_dtype", [(torch.float16, None), (torch.bfloat16, None),
+                                             (torch.float16, torch.float32), (torch.bfloat16, torch.float32)])
+def test_paged_prefill_invalid_block_id_gives_nan(dtype, out_dtype):
+    # the NaNs are written as bit patterns (the kernel has no NaN arithmetic):
+    # every element of the head's rows is a quiet NaN of the output type
     from tinyvllm_amd.attention import flash_prefill_paged
-    k, v, kc, vc, table = _paged_case(5, 80, 2, 64, 16, torch.float16)
+    k, v, kc, vc, table = _paged_case(5, 80, 2, 64, 16, dtype)
     table[2] = kc.shape[0] + 7
-    q = randn(98, 16, 8, 64, dtype=torch.float16)
-    out = flash_prefill_paged(q.cuda(), kc.cuda(), vc.cuda(), torch.from_numpy(table).cuda(), 64, True)
+    q = randn(98, 16, 8, 64, dtype=dtype)
+    out = flash_prefill_paged(q.cuda(), kc.cuda(), vc.cuda(), torch.from_numpy(table).cuda(), 64, True,
+                              out_dtype=out_dtype)
     torch.cuda.synchronize()
+    assert out.dtype == (dtype if out_dtype is None else out_dtype)
     assert torch.isnan(out.float()).all()
 
 

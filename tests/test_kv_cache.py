@@ -219,3 +219,30 @@ def test_prefill_slot_mapping_drives_fused_write():
         pos += n
     assert torch.equal(fused.k_cache[0], looped.k_cache[0])
     assert torch.equal(fused.v_cache[0], looped.v_cache[0])
+
+
+def test_config2_slot_map_fused_write_bit_exact():
+    """The bench's own config-2 workload (tinyvllm_amd.workloads.prefill_tinyllama_l512_l1024):
+    1536 tokens of seeded fp16 K/V written through its seeded shuffled slot map
+    (prompts of 512 and 1024 tokens, block 16, Hkv 4, head_dim 64), one fused
+    write per prompt exactly as bench.py times it, then every cache element
+    compared bit for bit with the oracle's placement (kv_cache.py:34-38 over
+    the slots of llama.py:199-209)."""
+    from tinyvllm_amd import workloads
+    from tinyvllm_amd.kv_cache import reshape_and_cache
+    wl = workloads.prefill_tinyllama_l512_l1024()
+    assert sum(len(s) for s in wl.slots) == 1536
+    kc = torch.zeros((wl.num_blocks, 16, 4, 64), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    for k, v, s in zip(wl.k, wl.v, wl.slots_dev):
+        reshape_and_cache(kc, vc, k[0], v[0], s)
+    torch.cuda.synchronize()
+    kr = np.zeros((wl.num_blocks, 16, 4, 64), np.float16)
+    vr = np.zeros_like(kr)
+    for k, v, s in zip(wl.k, wl.v, wl.slots):
+        reshape_and_cache_ref(kr, vr, k[0].cpu().numpy(), v[0].cpu().numpy(), s)
+    assert np.array_equal(kc.cpu().numpy().view(np.uint16), kr.view(np.uint16))
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), vr.view(np.uint16))
+    # the slots are distinct and every written row is a prompt row
+    allslots = np.concatenate(wl.slots)
+    assert len(np.unique(allslots)) == allslots.size

@@ -1,41 +1,27 @@
-"""Index arithmetic of the paged prefill kernel, restated on the CPU.
+"""Index arithmetic of the paged prefill kernel, checked on the CPU with the
+kernel's own code.
 
 `prefill_fa_kernel<..., PAGED = true>` (tinyvllm_amd/csrc/flash_prefill.hip)
-stages the block ids of a work-group's key range [kbeg, kstage) in LDS and
-maps every key a K/V load touches -- padded rows of a partial tile and the
-unconditional prefetch of tiles past the last one included -- to a staged
-slot.  This file restates that mapping and checks that every slot index stays
-inside the staged range for the shapes the GPU tests and the bench launch,
-for both key-tile widths (32 and 64).  The earlier clamp (to the last key of
-the sequence instead of the last staged key) is planted and must fail.
+stages the block ids of a work-group's key range in LDS and maps every key a
+K/V load touches -- padded rows of a partial tile and the re-requests of the
+last tile included -- to a staged slot, through the `__host__ __device__`
+functions of tinyvllm_amd/csrc/tv_paged_keys.h.  `paged_index_check.cpp`
+compiles those functions for the host (hipcc, no GPU code) and checks every
+slot for the shapes the GPU tests and the bench launch, for every kernel shape
+(1 / 2 / 4 key groups, 32- / 64-key tiles).  A former clamp (to the last key of
+the sequence instead of the last staged key) is planted through the driver and
+must be caught.
 """
+
+import shutil
+import subprocess
+from pathlib import Path
 
 import pytest
 
-
-def cdiv(a, b):
-    return -(-a // b)
-
-
-def staged_slots(q_len, start, bs, causal, bn, clamp_to_kv_len=False, rows=64):
-    """Yield (slot index, staged count) for every key a work-group's K/V loads touch."""
-    kv_len = start + q_len
-    lg = bs.bit_length() - 1
-    assert 1 << lg == bs
-    for qt in range(cdiv(q_len, rows)):
-        kend = min(kv_len, (qt + 1) * rows + start) if causal else kv_len
-        kbeg = 0
-        ntiles = cdiv(kend - kbeg, bn)
-        kstage = max(kend, kbeg + 1)                 # keys whose block ids are staged: [kbeg, kstage)
-        blk0 = kbeg >> lg
-        nblk = ((kstage - 1) >> lg) - blk0 + 1
-        hi = kv_len - 1 if clamp_to_kv_len else kstage - 1
-        # tiles 0 .. ntiles-1, plus prefetches of later tiles that re-read the last one
-        for t in list(range(ntiles)) + [ntiles - 1]:
-            for row in range(bn):
-                key = max(kbeg, min(kbeg + t * bn + row, hi))
-                yield (key >> lg) - blk0, nblk
-
+HERE = Path(__file__).resolve().parent
+CSRC = HERE.parent / "tinyvllm_amd" / "csrc"
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 CASES = [
     # (q_len, start_pos, block_size, causal): the GPU tests' shapes and the bench's
@@ -45,15 +31,29 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("bn", [32, 64])
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    if not Path(HIPCC).exists():
+        pytest.skip("hipcc not available")
+    exe = tmp_path_factory.mktemp("paged_index") / "paged_index_check"
+    res = subprocess.run([HIPCC, "-O1", "-std=c++17", f"-I{CSRC}", str(HERE / "paged_index_check.cpp"), "-o", str(exe)],
+                         capture_output=True, text=True)
+    assert res.returncode == 0, res.stdout + res.stderr
+    return exe
+
+
+def run(exe, q_len, start, bs, causal, planted=False):
+    args = [str(exe), str(q_len), str(start), str(bs), "1" if causal else "0"] + (["planted"] if planted else [])
+    return subprocess.run(args, capture_output=True, text=True)
+
+
 @pytest.mark.parametrize("q_len,start,bs,causal", CASES)
-def test_every_touched_key_maps_to_a_staged_slot(q_len, start, bs, causal, bn):
-    for idx, nblk in staged_slots(q_len, start, bs, causal, bn):
-        assert 0 <= idx < nblk
-        assert nblk <= 4096      # the kernel's LDS table size
+def test_every_touched_key_maps_to_a_staged_slot(checker, q_len, start, bs, causal):
+    res = run(checker, q_len, start, bs, causal)
+    assert res.returncode == 0 and res.stdout.startswith("ok "), res.stdout + res.stderr
+    assert int(res.stdout.split()[1]) > 0
 
 
-def test_the_old_clamp_reads_past_the_staged_table():
-    bad = [(idx, nblk) for idx, nblk in staged_slots(77, 300, 16, True, 64, clamp_to_kv_len=True)
-           if not 0 <= idx < nblk]
-    assert bad, "the planted clamp should reach an unstaged slot"
+def test_the_old_clamp_reads_past_the_staged_table(checker):
+    res = run(checker, 77, 300, 16, True, planted=True)
+    assert res.returncode == 1 and "slot" in res.stdout, res.stdout + res.stderr

@@ -98,6 +98,41 @@ def test_noalloc_equals_workspace_entry(first, second):
         assert torch.equal(got, want)
 
 
+def test_noalloc_replays_in_a_captured_graph():
+    """Captured in a HIP graph after one eager call on the device (which looks
+    the scratch address up), then replayed three times.  Between replays an
+    eager no-allocation call on a different, smaller input overwrites the
+    shared scratch, and the output is poisoned with NaN: every replay must still
+    equal tv_paged_decode bit for bit (the kernels write every scratch element
+    they read back, and the graph holds no memset node)."""
+    L = _lib()
+    lib = L.load()
+    spec = (16, 32, 8, 128, 16, 8192, 1024, torch.bfloat16)
+    other = (5, 32, 8, 128, 16, 3000, 1024, torch.bfloat16)
+    batch, hq, hkv, d, bs, ctx_max, partition, dtype = spec
+    q, kc, vc, bt, ctx = _case(200, batch, hq, hkv, d, bs, ctx_max, dtype)
+    want = _with_workspace(q, kc, vc, bt, ctx, partition)
+    first = _noalloc(q, kc, vc, bt, ctx, partition)         # the device's first call runs eagerly
+    torch.cuda.synchronize()
+    assert torch.equal(first, want)
+    oq, okc, ovc, obt, octx = _case(201, *other[:6], other[7])
+    owant = _with_workspace(oq, okc, ovc, obt, octx, other[6])
+    out = torch.full_like(q, float("nan"))
+    args = _args(q, kc, vc, bt, ctx, out, partition)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        L.check(lib.tv_paged_decode_noalloc(*args, L.stream_ptr(q.device)), "tv_paged_decode_noalloc (capture)")
+    for replay in range(3):
+        print(f"noalloc graph replay {replay}", flush=True)
+        mid = _noalloc(oq, okc, ovc, obt, octx, other[6])     # overwrites the scratch between replays
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(mid, owant), replay
+        assert torch.isfinite(out.float()).all(), replay
+        assert torch.equal(out, want), replay
+
+
 def test_noalloc_rejects_launches_beyond_the_scratch():
     """A launch needing more than 16 MiB of partials fails with TV_EINVAL."""
     L = _lib()

@@ -72,19 +72,13 @@ template <> __device__ __forceinline__ f32x4 mfma_frag<float>(u32x4 a, u32x4 b, 
   return c;
 }
 
-#ifndef TV_LINEAR_MIN_BLOCKS
-#define TV_LINEAR_MIN_BLOCKS 1
-#endif
-#ifndef TV_LINEAR_WSTAGES
-#define TV_LINEAR_WSTAGES 2
-#endif
+constexpr int kLinearMinBlocks = 1;    // occupancy hint of the product kernel
+constexpr int kLinearWStages = 2;      // W chunks in registers: in flight + the one multiplied
 // A chunks requested ahead of the one being multiplied.  Two ahead measured
 // slower for every product of the TinyLlama batch-64 decode step (64-step
 // graph: 1468 us/step at one ahead; two ahead for the SwiGLU product 1488, for
 // the split-K partial products 1485, for both 1505), so one it is.
-#ifndef TV_LINEAR_ASTAGES
-#define TV_LINEAR_ASTAGES 1
-#endif
+constexpr int kLinearAStages = 1;
 
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 constexpr int lcm3(int a, int b, int c) {
@@ -144,7 +138,7 @@ __device__ __forceinline__ void linear_epilogue(const LinearParams& p, const f32
 }
 
 template <typename T, int EPI>
-__global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const LinearParams p) {
+__global__ void __launch_bounds__(256, kLinearMinBlocks) linear_kernel(const LinearParams p) {
   // LDS in 16-bit units; a chunk row is 512 bytes of K at a 544-byte pitch (an
   // odd multiple of 32 modulo 256: conflict-free 16-byte reads)
   constexpr int KP = 256 + 16;
@@ -232,8 +226,8 @@ __global__ void __launch_bounds__(256, TV_LINEAR_MIN_BLOCKS) linear_kernel(const
     }
   };
 
-  constexpr int NWS = TV_LINEAR_WSTAGES;   // W chunks in registers: in flight + the one multiplied
-  constexpr int NAS = TV_LINEAR_ASTAGES;   // A chunks in flight in registers
+  constexpr int NWS = kLinearWStages;
+  constexpr int NAS = kLinearAStages;     // A chunks in flight in registers
   constexpr int U = lcm3(NWS, NAS, 2);     // loop unroll: every stage / buffer index compile-time
   u32x4 w[NWS][8], ar[NAS][8];
   bool av[NAS];

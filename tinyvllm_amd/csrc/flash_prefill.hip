@@ -18,6 +18,7 @@
 //  * prefill_generic_kernel<T>: any D, Dv <= 256, any element type (fp32 path and
 //    odd head sizes).  One wave per (query row, head); 64 keys per step.
 #include "tv_common.h"
+#include "tv_paged_keys.h"
 #include "tv_params.h"
 
 #include <algorithm>
@@ -39,14 +40,11 @@ __device__ __forceinline__ int prefill_head(int x, int num_heads, int remap) {
 }
 
 constexpr int kPrefillBM = 64;   // query rows per work unit (16 per wave)
-#ifndef TV_PREFILL_BN
-#define TV_PREFILL_BN 64
-#endif
-constexpr int kPrefillBN = TV_PREFILL_BN;   // keys per unit of the chunking and of prefill_key_tiles
+constexpr int kPrefillBN = 64;   // keys per unit of the chunking and of prefill_key_tiles
 
 // Key tiles query tile qt needs (causal rows stop at the diagonal).
 __device__ __forceinline__ int prefill_key_tiles(const PrefillParams& p, int qt) {
-  const int kend = p.causal ? min(p.kv_len, (qt + 1) * kPrefillBM + p.q_pos_offset) : p.kv_len;
+  const int kend = prefill_unit_key_end(p.causal != 0, p.kv_len, qt, kPrefillBM, p.q_pos_offset);
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
@@ -71,6 +69,19 @@ __device__ __forceinline__ void prefill_unit(const PrefillParams& p, int u, int&
   }
   nchunks = (prefill_key_tiles(p, qt) + p.chunk_tiles - 1) / p.chunk_tiles;
   chunk = u;
+}
+
+// Store 4 quiet NaNs as out_dtype, as bit patterns written by integer stores:
+// the prefill kernels are compiled without NaN semantics, so a NaN produced by
+// floating-point arithmetic there is undefined.
+__device__ __forceinline__ void store4_nan(void* base, size_t idx, int out_dtype) {
+  if (out_dtype == kF32) {
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint32_t*>(base) + idx) =
+        u32x4{0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u};
+  } else {
+    const uint32_t w = out_dtype == kF16 ? 0x7E007E00u : 0x7FC07FC0u;
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(base) + idx) = u32x2{w, w};
+  }
 }
 
 // Store 4 consecutive output elements (a row slice of one query) as out_dtype.
@@ -118,25 +129,10 @@ template <int KB> __device__ __forceinline__ float max_tile(const f32x4 (&st)[KB
   return t[0];
 }
 
-#ifndef TV_PREFILL_RB
-#define TV_PREFILL_RB 2       // 16-row query blocks per wave (head_dim 64)
-#endif
-#ifndef TV_PREFILL_KS
-#define TV_PREFILL_KS 2       // key-tile groups per work-group (head_dim 64)
-#endif
-#ifndef TV_PREFILL_FA_BN
-#define TV_PREFILL_FA_BN 64
-#endif
-#ifndef TV_PREFILL_WAVES_PER_EU
-#define TV_PREFILL_WAVES_PER_EU 2
-#endif
-
-// Block ids of a paged prompt staged in LDS per work-group (keys of up to
-// kPagedTableMax blocks: 65536 tokens at block size 16).
-constexpr int kPagedTableMax = 4096;
+constexpr int kPrefillWavesPerEu = 2;   // occupancy the VGPR budget of the 64-row kernel allows
 
 template <typename T, int D, int RB, int KS, int BN, bool PAGED>
-__global__ void __launch_bounds__(256 / RB * KS) __attribute__((amdgpu_waves_per_eu(TV_PREFILL_WAVES_PER_EU)))
+__global__ void __launch_bounds__(256 / RB * KS) __attribute__((amdgpu_waves_per_eu(kPrefillWavesPerEu)))
 prefill_fa_kernel(const PrefillParams pa) {
   // Several prompts per launch: this work-group's prompt is seq_order[blockIdx.z];
   // its rows become the whole problem (pointers and lengths rebased).  Chunked
@@ -194,7 +190,7 @@ prefill_fa_kernel(const PrefillParams pa) {
   const int kbeg = kt0 * kPrefillBN;
   const int klim = min(kt1 * kPrefillBN, p.kv_len);                 // end before the causal limit
   const int qoff = p.q_pos_offset;
-  const int kend = p.causal ? min(klim, (qt + 1) * BM + qoff) : klim;
+  const int kend = prefill_unit_key_end(p.causal != 0, klim, qt, BM, qoff);
   const int ntiles = (kend - kbeg + BN - 1) / BN;
   const float c = p.scale * kLog2e;
   const int row0 = qt * BM + wave * RB * 16;   // first query row of this wave
@@ -239,9 +235,9 @@ prefill_fa_kernel(const PrefillParams pa) {
   const int blk0 = kbeg >> lg;
   __shared__ int sbad;
   bool bad = false;
-  const int kstage = max(kend, kbeg + 1);     // keys whose block ids are staged: [kbeg, kstage)
+  const int kstage = paged_stage_end(kbeg, kend);   // keys whose block ids are staged: [kbeg, kstage)
   if constexpr (PAGED) {
-    const int nblk = ((kstage - 1) >> lg) - blk0 + 1;
+    const int nblk = paged_staged_blocks(kbeg, kstage, lg);
     if (threadIdx.x == 0) sbad = 0;
     lds_barrier();
     for (int i = threadIdx.x; i < nblk; i += blockDim.x) {
@@ -256,7 +252,7 @@ prefill_fa_kernel(const PrefillParams pa) {
   struct Stage {
     u32x4 k[NV], v[NV];
   };
-  auto tile_of = [&](int j) { return min(grp + KS * j, ntiles - 1); };
+  auto tile_of = [&](int j) { return prefill_group_tile(grp, KS, j, ntiles); };
   // per-tile buffer resources: base at the tile's first row, range ending at
   // the last key row, so rows past kv_len read as zero (byte quantities in
   // scalar registers, one multiply per tile)
@@ -273,8 +269,8 @@ prefill_fa_kernel(const PrefillParams pa) {
       // last staged key: the table is in LDS for keys [kbeg, kend) only
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const int key = max(kbeg, min(kbeg + (int)t * BN + koff[i], kstage - 1));
-        const long long row = ((long long)stbl[(key >> lg) - blk0] << lg) + (key & ((1 << lg) - 1));
+        const int key = paged_load_key(kbeg, kstage, (int)t, BN, koff[i]);
+        const long long row = ((long long)stbl[paged_stage_slot(key, kbeg, lg)] << lg) + (key & ((1 << lg) - 1));
         s.k[i] = *reinterpret_cast<const u32x4*>(kbase + row * p.k_stride + voff[i]);
         s.v[i] = *reinterpret_cast<const u32x4*>(vbase + row * p.v_stride + voff[i]);
       }
@@ -483,12 +479,14 @@ prefill_fa_kernel(const PrefillParams pa) {
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
     if (qi[r] >= p.q_len) continue;
-    const float inv = bad ? __builtin_nanf("") : 1.0f / lfin[r];
+    const float inv = 1.0f / lfin[r];
     if (nchunks == 1) {
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-        store4<T>(p.out, (size_t)qi[r] * p.out_stride + (size_t)h * D + db * 16 + 4 * g, oacc[r][db] * inv,
-                  p.out_dtype);
+      for (int db = 0; db < DB; ++db) {
+        const size_t idx = (size_t)qi[r] * p.out_stride + (size_t)h * D + db * 16 + 4 * g;
+        if (bad) store4_nan(p.out, idx, p.out_dtype);    // a block id outside the cache
+        else store4<T>(p.out, idx, oacc[r][db] * inv, p.out_dtype);
+      }
     } else {
       const size_t unit = ((size_t)h * nqt + qt) * p.max_chunks + chunk;
       const int row = qi[r] - qt * BM;
@@ -638,7 +636,7 @@ void prefill_units(const PrefillParams& p, int& units, int& max_chunks) {
   units = 0;
   max_chunks = 1;
   for (int qt = 0; qt < nqt; ++qt) {
-    const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM + p.q_pos_offset) : p.kv_len;
+    const int kend = prefill_unit_key_end(p.causal != 0, p.kv_len, qt, kPrefillBM, p.q_pos_offset);
     const int nkt = (kend + kPrefillBN - 1) / kPrefillBN;
     const int ch = (nkt + p.chunk_tiles - 1) / p.chunk_tiles;
     units += ch;
@@ -667,7 +665,7 @@ size_t prefill_workspace_bytes(const PrefillParams& p, int dtype) {
 
 // Key tiles of the last query tile (the longest causal row), host side.
 int prefill_key_tiles_host(const PrefillParams& p, int qt) {
-  const int kend = p.causal ? std::min(p.kv_len, (qt + 1) * kPrefillBM + p.q_pos_offset) : p.kv_len;
+  const int kend = prefill_unit_key_end(p.causal != 0, p.kv_len, qt, kPrefillBM, p.q_pos_offset);
   return (kend + kPrefillBN - 1) / kPrefillBN;
 }
 
@@ -677,11 +675,6 @@ int prefill_key_tiles_host(const PrefillParams& p, int qt) {
 template <typename T, int D, bool PAGED = false>
 void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) {
   constexpr int BN = D == 64 ? 64 : 32;
-#ifdef TV_PREFILL_FIXED
-  (void)cfg;
-  hipLaunchKernelGGL((prefill_fa_kernel<T, D, TV_PREFILL_RB, TV_PREFILL_KS, TV_PREFILL_FA_BN, PAGED>), grid,
-                     dim3(256 / TV_PREFILL_RB * TV_PREFILL_KS), 0, stream, pp);
-#else
   if constexpr (D == 64) {
     if (cfg == 3) {
       hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 4, 32, PAGED>), grid, dim3(1024), 0, stream, pp);
@@ -691,7 +684,6 @@ void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) 
   if (cfg == 0 || cfg == 3) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, BN, PAGED>), grid, dim3(512), 0, stream, pp);
   else if (cfg == 2) hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 2, 32, PAGED>), grid, dim3(512), 0, stream, pp);
   else hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 1, BN, PAGED>), grid, dim3(256), 0, stream, pp);
-#endif
 }
 
 // 128-row work-groups with LDS-DMA tiles (prefill_rows_kernel,
@@ -699,16 +691,9 @@ void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) 
 // faster (MI355X, Hq 32 / Hkv 8: L 2048 54-56 against 64-68 us, L 4096
 // 174 against 207-210); below 2048 rows, or at head_dim 64, this file's 64-row
 // kernel wins.
-#ifndef TV_PREFILL_ROWS_MODE
-#define TV_PREFILL_ROWS_MODE 1     // 0: never, 1: long head_dim-128 prompts, 2: always (when the shape allows)
-#endif
 constexpr int kRowsMinLen = 2048;
 
-bool use_rows_kernel(int head_dim, long long max_q_len) {
-  if (TV_PREFILL_ROWS_MODE == 0) return false;
-  if (TV_PREFILL_ROWS_MODE == 2) return true;
-  return head_dim == 128 && max_q_len >= kRowsMinLen;
-}
+bool use_rows_kernel(int head_dim, long long max_q_len) { return head_dim == 128 && max_q_len >= kRowsMinLen; }
 
 // Returns 0 on launch, 1 if the shape has no kernel, 2 if the workspace is missing.
 int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, size_t workspace_bytes,

@@ -23,8 +23,12 @@
 //    requested when the previous pair starts, and each pair is one step (one
 //    barrier, one softmax over its 64 keys).
 // The softmax is the 64-row kernel's: log2 domain, lazy rescale (threshold 8),
-// P kept in registers as the B operand of O^T = V^T P^T; the scale is applied
-// in fp32 after the product, s * scale * log2(e) - m in one fma (llama.py:84).
+// P kept in registers as the B operand of O^T = V^T P^T.  Where the scale
+// enters depends on the type (kPreScaleQ, tv_common.h): fp16 pre-scales Q by
+// scale * log2(e) and starts the score accumulator at -m, so scores leave the
+// matrix cores ready for exp2; bf16 keeps Q as given and applies
+// s * scale * log2(e) - m in one fp32 fma after the product, the reference's
+// order (llama.py:84).
 // Row sums of the rounded P accumulate per lane with v_dot2 against ones (VALU,
 // instead of an extra MFMA per tile) and are summed over the four lanes of a
 // query at the end.
@@ -71,6 +75,8 @@
 // 635 us against 60 / 198 / 630 us.
 #include "tv_common.h"
 #include "tv_params.h"
+#include "tv_device_cache.h"
+#include "tv_tile_dma.h"
 
 #include <type_traits>
 
@@ -81,56 +87,6 @@ namespace {
 constexpr int kRowsBM = 128;   // query rows per work-group
 constexpr int kRowsBN = 32;    // keys per tile
 constexpr int kRowsBuf = 4;    // tile buffers: two pairs
-
-// chunk permutation of tile row r (16-byte chunks; 16 per row at head_dim 128,
-// 8 at 64): distinct over any 16 consecutive rows for a fixed chunk (K reads),
-// and keeps the chunk pairs {2u, 2u+1} of 4 consecutive rows on distinct banks
-// (transposing V reads).
-template <int D> __device__ __forceinline__ int chunk_perm(int r) {
-  if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
-}
-
-// 16 bytes per lane from buffer `rsrc` at byte offset voff straight into LDS at
-// lds_base + 16 * lane (gfx950 LDS DMA).  The compiler does not see these
-// loads: callers wait for them with wait_vmcnt before a barrier.
-__device__ __forceinline__ void load_lds16(u32x4 rsrc, uint32_t lds_base, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_base), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-
-template <int N> __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-__device__ __forceinline__ uint32_t sgpr(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
-
-__device__ __forceinline__ u32x4 rsrc_words(const void* base, unsigned long long bytes) {
-  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-  // range clamped to 32 bits with a scalar compare of the high word (as C the
-  // compiler makes it a 64-bit vector compare plus readfirstlane)
-  uint32_t n;
-  asm("s_cmp_lg_u32 %1, 0\n\ts_cselect_b32 %0, -1, %2"
-      : "=s"(n)
-      : "s"((uint32_t)(bytes >> 32)), "s"((uint32_t)bytes)
-      : "scc");
-  return u32x4{sgpr((uint32_t)a), sgpr((uint32_t)(a >> 32)), n, 0x00020000u};
-}
-
-template <typename T> constexpr uint32_t kRowsOnes2 = 0;
-template <> constexpr uint32_t kRowsOnes2<_Float16> = 0x3C003C00u;
-template <> constexpr uint32_t kRowsOnes2<__bf16> = 0x3F803F80u;
-
-// acc + the sum of the eight packed 16-bit values of p (fp32 accumulation)
-template <typename T> __device__ __forceinline__ float rowsum8(u32x4 p, float acc) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) acc = dot2<T>(p[w], kRowsOnes2<T>, acc);
-  return acc;
-}
 
 }  // namespace
 
@@ -221,7 +177,7 @@ prefill_rows_kernel(const PrefillParams pa) {
   for (int i = 0; i < NI; ++i) {
     const int row = (wave * NI + i) * RPI + lane / SPR;
     const int slot = lane % SPR;
-    const int chunk = slot ^ chunk_perm<D>(row);
+    const int chunk = slot ^ tile_chunk_perm<D>(row);
     kvoff[i] = (uint32_t)(row * kstr + chunk * 16);
     vvoff[i] = (uint32_t)(row * vstr + chunk * 16);
   }
@@ -271,12 +227,12 @@ prefill_rows_kernel(const PrefillParams pa) {
   // ((ks ^ fk) << 2) | (g ^ (f & 3)) with f = chunk_perm(col), fk = f >> 2; V
   // chunk 2 db + b of row r at ((db ^ fv) << 1) | (b ^ (f_r & 1)), fv = f_r >> 1:
   // one base and one XOR key per operand instead of a register per offset.
-  const int kperm = chunk_perm<D>(col);
+  const int kperm = tile_chunk_perm<D>(col);
   const int kofs0 = col * ROWB + ((g ^ (kperm & 3)) << 4);
   const int kkey = kperm >> 2;
   auto koff = [&](int ks) { return kofs0 + ((ks ^ kkey) << 6); };
   const int vrow = 4 * g + (col >> 2);
-  const int vperm = chunk_perm<D>(vrow);
+  const int vperm = tile_chunk_perm<D>(vrow);
   const int vofs0 = TILEB + vrow * ROWB + ((((col & 3) >> 1) ^ (vperm & 1)) << 4) + 8 * (col & 1);
   const int vkey = vperm >> 1;
   auto voff = [&](int db) { return vofs0 + ((db ^ vkey) << 5); };
@@ -441,18 +397,8 @@ prefill_rows_kernel(const PrefillParams pa) {
 // device (occupancy x CUs), queried once per device.
 template <typename T, int D>
 long long rows_resident() {
-  static long long cache[16] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
-  if (cache[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prefill_rows_kernel<T, D>, 256, 0) != hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-    cache[dev] = (long long)per_cu * cus;
-  }
-  return cache[dev];
+  static std::atomic<long long> slots[kMaxDevices];
+  return resident_work_groups(slots, prefill_rows_kernel<T, D>, 256);
 }
 
 template <typename T, int D>

@@ -313,13 +313,12 @@ int run_layers(const tv_llama_model* m, const tv_llama_cache* c, const LayerIO& 
   return TV_OK;
 }
 
+// Work-groups a skinny product aims for when it splits K.
+constexpr long long kLinearTargetWorkGroups = 192;
+
 }  // namespace
 
 extern "C" {
-
-#ifndef TV_LINEAR_TARGET_WGS
-#define TV_LINEAR_TARGET_WGS 192
-#endif
 
 int tv_linear_k_split(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 32;
@@ -328,7 +327,7 @@ int tv_linear_k_split(int M, int N, int K) {
   // About three work-groups per four CUs: more splits add partials that the
   // consumer (norm or step attention) reads back, and on the TinyLlama step
   // 192 beat 128, 160, 224 and 256 (1.53 vs 1.55-1.59 ms).
-  const long long target = TV_LINEAR_TARGET_WGS;
+  const long long target = kLinearTargetWorkGroups;
   if (tiles >= target / 2) return (int)full;
   const long long want = (target + tiles - 1) / tiles;
   const long long per = (K + want - 1) / want;

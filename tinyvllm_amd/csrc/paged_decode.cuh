@@ -39,24 +39,13 @@
 
 #include "tv_common.h"
 
-// Build-time tuning knobs (defaults are the tuned values for gfx950).
-#ifndef TV_DECODE_TILE_MUL
-#define TV_DECODE_TILE_MUL 1     // rows per lane per tile multiplier (tile = 16 * this tokens)
-#endif
-#ifndef TV_DECODE_NT
-#define TV_DECODE_NT 1           // non-temporal K/V loads
-#endif
-#ifndef TV_DECODE_ACC_MAX
-#define TV_DECODE_ACC_MAX 64     // max fp32 accumulators per lane (sets lanes per row)
-#endif
-#ifndef TV_DECODE_MIN_BLOCKS
-#define TV_DECODE_MIN_BLOCKS 1   // occupancy hint: work-groups per CU the VGPR budget must allow
-#endif
-#ifndef TV_DECODE_BT_PREFETCH
-#define TV_DECODE_BT_PREFETCH 0  // look the next tile's block id up one tile ahead
-#endif
-
 namespace tv {
+
+// Shape constants, measured on MI355X: at most 64 fp32 accumulators per lane
+// (sets the lanes per cache row), 16-token tiles, and the VGPR budget sized for
+// one work-group per CU.
+constexpr int kDecodeAccMax = 64;
+constexpr int kDecodeMinBlocks = 1;
 
 struct DecodeParams {
   void* out;                 // [B, Hq, D] in out_dtype
@@ -103,11 +92,11 @@ template <typename T, int D, int GT>
 struct DecodeShape {
   static constexpr int ROW_BYTES = D * (int)sizeof(T);
   static constexpr int MAXL = ROW_BYTES / 16 < 16 ? ROW_BYTES / 16 : 16;
-  static constexpr int WANT = D * GT / TV_DECODE_ACC_MAX < 1 ? 1 : D * GT / TV_DECODE_ACC_MAX;
+  static constexpr int WANT = D * GT / kDecodeAccMax < 1 ? 1 : D * GT / kDecodeAccMax;
   static constexpr int LPR = WANT < MAXL ? WANT : MAXL;
   static constexpr int VPL = ROW_BYTES / (16 * LPR);
   static constexpr int RPI = 64 / LPR;
-  static constexpr int NR = (RPI >= 16 ? 1 : 16 / RPI) * TV_DECODE_TILE_MUL;
+  static constexpr int NR = RPI >= 16 ? 1 : 16 / RPI;
   static constexpr int TT = RPI * NR;
   static constexpr int EPV = 16 / (int)sizeof(T);
   static constexpr int EPL = VPL * EPV;
@@ -115,17 +104,13 @@ struct DecodeShape {
 };
 
 // 16-byte cache-row load; K/V rows are read exactly once per launch, so they
-// can bypass cache retention (TV_DECODE_NT).
+// bypass cache retention (non-temporal).
 __device__ __forceinline__ u32x4 load_row16(const void* ptr) {
-#if TV_DECODE_NT
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
-#else
-  return *reinterpret_cast<const u32x4*>(ptr);
-#endif
 }
 
 __device__ __forceinline__ u32x4 buffer_load_nt16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, TV_DECODE_NT ? 2 : 0));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2));
 }
 
 // Whether every TT-token tile of a launch lies in one cache block (one
@@ -256,15 +241,14 @@ __device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D
 
   // Fetch the K/V rows of the tile starting at token t0 (rows past `end` or in
   // an invalid block are zero and marked invalid).
-  constexpr bool kBtAhead = TV_DECODE_BT_PREFETCH;
-  auto fetch = [&](int t0, int blk_ahead, u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR]) {
+  auto fetch = [&](int t0, u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR]) {
     if constexpr (UB) {
       // The whole tile lies in one cache block: one wave-uniform table lookup,
       // then buffer loads from the tile's first row.  The buffer's range ends
       // at the last attended row of the tile (nothing when the block id is
       // invalid), so rows past it read as zero without per-row branches, and
       // the lane offsets are the same for every tile.
-      const int blk = kBtAhead ? blk_ahead : bt[t0 >> p.bs_log2];
+      const int blk = bt[t0 >> p.bs_log2];
       const bool blk_ok = (unsigned)blk < (unsigned)p.num_blocks;
       bad |= !blk_ok;
       const int rows = blk_ok ? min(TT, end - t0) : 0;
@@ -402,14 +386,10 @@ __device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D
     }
   };
 
-  int blk_next = 0;
-  if (kBtAhead && UB && start + wi * TT < end) blk_next = bt[(start + wi * TT) >> p.bs_log2];
   for (int t0 = start + wi * TT; t0 < end; t0 += wph * TT) {
     u32x4 kr[NR][VPL], vr[NR][VPL];
     bool valid[NR];
-    const int blk_cur = blk_next;
-    if (kBtAhead && UB && t0 + wph * TT < end) blk_next = bt[(t0 + wph * TT) >> p.bs_log2];
-    fetch(t0, blk_cur, kr, vr, valid);
+    fetch(t0, kr, vr, valid);
     consume(kr, vr, valid);
   }
 
@@ -492,7 +472,7 @@ __device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D
 
 // One work-group per (partition, KV head x query-head chunk, sequence).
 template <typename T, int D, int GT, int NW, bool UB>
-__global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_kernel(const DecodeParams p) {
+__global__ void __launch_bounds__(64 * NW, kDecodeMinBlocks) paged_decode_kernel(const DecodeParams p) {
   __shared__ DecodeSmem<D, GT, NW> sm;
   const int part = blockIdx.x;
   const int b = blockIdx.z;
@@ -515,7 +495,7 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_ke
 // first.  The grid has one work-group per item at hpw = 1; with head pairs the
 // upper half, dispatched last, has no item and exits.
 template <typename T, int D, int GT, int NW, int HPW, bool UB>
-__global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_scheduled_kernel(const DecodeParams p) {
+__global__ void __launch_bounds__(64 * NW, kDecodeMinBlocks) paged_decode_scheduled_kernel(const DecodeParams p) {
   __shared__ DecodeSmem<D, GT, NW> sm;
   const int hpw = HPW > 1 ? p.sched[0] : 1;
   const int rows = p.num_kv_heads / hpw * p.head_chunks;
@@ -533,10 +513,9 @@ __global__ void __launch_bounds__(64 * NW, TV_DECODE_MIN_BLOCKS) paged_decode_sc
 // the main kernel and are skipped here.
 __global__ void __launch_bounds__(64) paged_decode_reduce_kernel(const DecodeParams p, int head_dim);
 
-#ifndef TV_DECODE_PAIR_SPREAD
-#define TV_DECODE_PAIR_SPREAD 3
-#endif
-constexpr int kDecodePairSpread = TV_DECODE_PAIR_SPREAD;
+// KV heads are paired in the scheduled launch when the longest context is at
+// least this many times the shortest (decode_order_kernel).
+constexpr int kDecodePairSpread = 3;
 __global__ void __launch_bounds__(1024) decode_order_kernel(const int* context_lens, int num_seqs, int width,
                                                             int pair_ok, int* sched);
 

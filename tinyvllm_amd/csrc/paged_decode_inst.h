@@ -4,51 +4,27 @@
 #pragma once
 
 #include "paged_decode.cuh"
+#include "tv_device_cache.h"
 
 namespace tv {
 
-#ifndef TV_DECODE_WAVES
-#define TV_DECODE_WAVES 4
-#endif
-constexpr int kDecodeWaves = TV_DECODE_WAVES;   // waves per work-group
+constexpr int kDecodeWaves = 4;   // waves per work-group
 
 // Work-groups of the paired scheduled kernel resident at once on the current
 // device (occupancy x CUs), queried once per device and instantiation.
 template <typename T, int D, int GT, bool UB>
 int scheduled_pair_slots() {
-  static int cache[16] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
-  if (cache[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, paged_decode_scheduled_kernel<T, D, GT, kDecodeWaves, 2, UB>, 64 * kDecodeWaves, 0) !=
-            hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-    cache[dev] = per_cu * cus;
-  }
-  return cache[dev];
+  static std::atomic<long long> slots[kMaxDevices];
+  return (int)resident_work_groups(slots, paged_decode_scheduled_kernel<T, D, GT, kDecodeWaves, 2, UB>,
+                                   64 * kDecodeWaves);
 }
 
 // Work-groups of the partitioned kernel (uniform-tile form) resident at once on
 // the current device (occupancy x CUs), queried once per device and instantiation.
 template <typename T, int D, int GT>
 int partitioned_slots() {
-  static int cache[16] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
-  if (cache[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<T, D, GT, kDecodeWaves, true>,
-                                                     64 * kDecodeWaves, 0) != hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-    cache[dev] = per_cu * cus;
-  }
-  return cache[dev];
+  static std::atomic<long long> slots[kMaxDevices];
+  return (int)resident_work_groups(slots, paged_decode_kernel<T, D, GT, kDecodeWaves, true>, 64 * kDecodeWaves);
 }
 
 template <typename T>

@@ -381,12 +381,8 @@ bool step_attn_supported(int head_dim, int group, int block_size) {
   return (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 16 && block_size % 16 == 0;
 }
 
-#ifndef TV_STEP_ATTN_W64
-#define TV_STEP_ATTN_W64 6    // waves per work-group at head_dim 64
-#endif
-#ifndef TV_STEP_ATTN_PF64
-#define TV_STEP_ATTN_PF64 2   // tiles in flight per wave at head_dim 64
-#endif
+constexpr int kStepAttnWaves64 = 6;      // waves per work-group at head_dim 64
+constexpr int kStepAttnInFlight64 = 2;   // tiles in flight per wave at head_dim 64
 
 // head_dim 64: 6 waves and two tiles in flight per wave (TinyLlama step, batch
 // 64 x 4 KV heads, one work-group per CU: 1480 us/step against 1482 with one
@@ -394,7 +390,7 @@ bool step_attn_supported(int head_dim, int group, int block_size) {
 // 1543 with 12, 1548 with 16); head_dim 128: 4 waves, whose larger tiles need
 // more than the 256 registers two waves per SIMD allow.
 void launch_step_attn(const StepAttnParams& p, int head_dim, int dtype, hipStream_t s) {
-  constexpr int W64 = TV_STEP_ATTN_W64, PF64 = TV_STEP_ATTN_PF64;
+  constexpr int W64 = kStepAttnWaves64, PF64 = kStepAttnInFlight64;
   const dim3 grid(p.Hkv, p.B);
   if (dtype == kF16) {
     if (head_dim == 64) hipLaunchKernelGGL((step_attn_kernel<_Float16, 64, W64, PF64>), grid, dim3(64 * W64), 0, s, p);

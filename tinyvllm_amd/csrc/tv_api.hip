@@ -10,6 +10,7 @@
 #include "../../include/tv_attn.h"
 #include "paged_decode_inst.h"
 #include "tv_error.h"
+#include "tv_device_cache.h"
 #include "tv_params.h"
 
 namespace tv {
@@ -46,6 +47,7 @@ const char* last_error() { return g_err.c_str(); }
 namespace {
 
 using tv::check_launch;
+using tv::kMaxDevices;
 using tv::fail;
 using tv::ok;
 
@@ -58,13 +60,11 @@ int ilog2(long long x) {
   return r;
 }
 
-#ifndef TV_DECODE_GT_MAX
-#define TV_DECODE_GT_MAX 8
-#endif
-
-// Largest power of two <= TV_DECODE_GT_MAX that divides the GQA group.
+// Query heads of a GQA group that one decode work-group serves: the largest
+// power of two <= 8 that divides the group.
+constexpr int kDecodeGroupMax = 8;
 int heads_per_group_chunk(int group) {
-  for (int gt = TV_DECODE_GT_MAX; gt > 1; gt >>= 1)
+  for (int gt = kDecodeGroupMax; gt > 1; gt >>= 1)
     if (group % gt == 0) return gt;
   return 1;
 }
@@ -93,7 +93,6 @@ int paged_decode_impl(const char* who, void* out, const void* queries, const voi
 constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
 __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
 
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 

@@ -395,11 +395,12 @@ class Llama:
         if len(seq_ids) != batch or len(pos) != batch:
             raise ValueError("seq_ids, start_positions and block_tables_tensor must have one entry per sequence")
         bs = kv_cache.block_size
-        cols = []
-        for sid, p in zip(seq_ids, pos):
+        for sid, p in zip(seq_ids, pos):                      # every check before any allocation
             if block_manager.get_context_length(sid) != p:
                 raise ValueError(f"sequence {sid}: start position {p} is not the block manager's position "
                                  f"{block_manager.get_context_length(sid)}")
+        cols = []
+        for sid, p in zip(seq_ids, pos):
             _, block_id, _ = block_manager.get_slot(sid)      # llama.py:382 (allocates on a block boundary)
             cols.append((p // bs, block_id))
         need = max(c for c, _ in cols) + 1
