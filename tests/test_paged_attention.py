@@ -203,8 +203,10 @@ def test_scheduled_launch_group_shapes(hq, hkv, d, dtype):
 
 def test_partition_size_recommendation():
     """tv_paged_decode_partition_size: whole context when the batch fills the
-    GPU, else partitions that make a full-width batch's work-groups fill the
-    resident work-group slots once; a multiple of 16, at least 64."""
+    GPU, and for small launches (at most one (sequence, KV head) pair per CU,
+    contexts of at most 512 tokens, one launch of wide work-groups); else
+    partitions that make a full-width batch's work-groups fill the resident
+    work-group slots once; a multiple of 16, at least 64."""
     from tinyvllm_amd.attention import default_partition_size
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     whole = default_partition_size(4 * cus // 8, 32, 8, 128, 256, 16, torch.float16)
@@ -213,7 +215,9 @@ def test_partition_size_recommendation():
     assert p % 16 == 0 and 64 <= p < 32768
     parts = -(-32768 // p)
     assert 16 * 8 * parts >= cus                    # at least one work-group per CU
-    assert default_partition_size(4, 32, 4, 64, 16, 16, torch.float32) == 64
+    assert default_partition_size(4, 32, 4, 64, 16, 16, torch.float32) == 256       # config 1: one launch
+    p = default_partition_size(4, 32, 4, 64, 64, 16, torch.float32)                 # 1024-token width: split
+    assert p % 16 == 0 and 64 <= p < 1024
     with pytest.raises(ValueError):
         default_partition_size(4, 30, 4, 64, 16, 16, torch.float32)
 

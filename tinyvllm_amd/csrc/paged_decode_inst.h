@@ -10,6 +10,19 @@ namespace tv {
 
 constexpr int kDecodeWaves = 4;   // waves per work-group
 
+// Small launches (at most one (sequence, KV head) pair per CU, contexts of at
+// most kDecodeWideTokens): one unsplit launch of 8-wave work-groups, so a
+// pair's tiles are spread over twice the waves (at most four 16-token tiles
+// each) and no merge launch follows; the waves merge through LDS (64 GT D
+// bytes).  Eight waves cap a wave at 256 VGPRs: the shapes with a wide form,
+// head_dim 64 or 128 with GQA chunks of 2+ heads, fit it without spills in all
+// three element types (others -- head_dim 256, fp32 head_dim 32 with 8 heads,
+// single heads of fp32 head_dim 128 -- would spill); sixteen waves (128 VGPRs)
+// would spill the larger GQA groups.
+constexpr int kDecodeWideWaves = 8;
+constexpr int kDecodeWideTokens = 512;
+template <int D, int GT> constexpr bool kDecodeWideOk = (D == 64 || D == 128) && GT >= 2;
+
 // Work-groups of the paired scheduled kernel resident at once on the current
 // device (occupancy x CUs), queried once per device and instantiation.
 template <typename T, int D, int GT, bool UB>
@@ -52,7 +65,8 @@ bool decode_pair_allowed(const DecodeParams& p, int head_dim, int gt);
 // kernel on `grid`.  Returns false when (D, GT) has no
 // instantiation.
 template <typename T>
-bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, bool pair, dim3 grid, hipStream_t stream);
+bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, bool pair, bool wide, dim3 grid,
+                         hipStream_t stream);
 
 #define TV_DECODE_SCHEDULED(T, D, GT, HPW, UB)                                                    \
   {                                                                                               \
@@ -70,6 +84,17 @@ bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, bool pair,
       if (pair) TV_DECODE_SCHEDULED(T, D, GT, 2, false)                                              \
       if (ub) TV_DECODE_SCHEDULED(T, D, GT, 1, true)                                                 \
       TV_DECODE_SCHEDULED(T, D, GT, 1, false)                                                        \
+    }                                                                                             \
+    if constexpr (kDecodeWideOk<D, GT>) {                                                         \
+      if (wide) {                                                                                 \
+        if (ub)                                                                                   \
+          hipLaunchKernelGGL((paged_decode_kernel<T, D, GT, kDecodeWideWaves, true>), grid,       \
+                             dim3(64 * kDecodeWideWaves), 0, stream, p);                          \
+        else                                                                                      \
+          hipLaunchKernelGGL((paged_decode_kernel<T, D, GT, kDecodeWideWaves, false>), grid,      \
+                             dim3(64 * kDecodeWideWaves), 0, stream, p);                          \
+        return true;                                                                              \
+      }                                                                                           \
     }                                                                                             \
     if (ub)                                                                                       \
       hipLaunchKernelGGL((paged_decode_kernel<T, D, GT, kDecodeWaves, true>), grid,               \
@@ -122,8 +147,8 @@ bool launch_paged_decode(const DecodeParams& p, int head_dim, int gt, bool pair,
     return false;                                                                                \
   }                                                                                              \
   template <>                                                                                    \
-  bool launch_paged_decode<T>(const DecodeParams& p, int head_dim, int gt, bool pair, dim3 grid, \
-                              hipStream_t stream) {                                              \
+  bool launch_paged_decode<T>(const DecodeParams& p, int head_dim, int gt, bool pair, bool wide,  \
+                              dim3 grid, hipStream_t stream) {                                   \
     TV_DECODE_ALL_GT(T, 16)                                                                      \
     TV_DECODE_ALL_GT(T, 32)                                                                      \
     TV_DECODE_ALL_GT(T, 64)                                                                      \

@@ -60,6 +60,19 @@ int ilog2(long long x) {
   return r;
 }
 
+// Whether a decode launch takes the wide work-groups (kDecodeWideWaves waves):
+// unsplit, at most one (sequence, KV head) row per CU, every context within
+// kDecodeWideTokens.  (Kernel shapes without a wide form, kDecodeWideOk, keep
+// the 4-wave work-groups.)
+bool decode_wide(int num_seqs, int rows_per_seq, long long width, int partition_size) {
+  if (partition_size < width || width > tv::kDecodeWideTokens) return false;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess || cus < 1)
+    return false;
+  return (long long)num_seqs * rows_per_seq <= cus;
+}
+
 // Query heads of a GQA group that one decode work-group serves: the largest
 // power of two <= 8 that divides the group.
 constexpr int kDecodeGroupMax = 8;
@@ -160,6 +173,7 @@ int tv_paged_decode_partition_size(int num_seqs, int num_heads, int num_kv_heads
                                                hipSuccess || cus < 1)
     return fail(TV_EHIP, "tv_paged_decode_partition_size: no device"), 0;
   if (rows >= 4LL * cus) return whole;
+  if (rows <= cus && width <= tv::kDecodeWideTokens) return whole;   // one launch of wide work-groups
   const int slots = dtype == TV_F32   ? tv::decode_partitioned_slots<float>(head_dim, gt)
                     : dtype == TV_F16 ? tv::decode_partitioned_slots<_Float16>(head_dim, gt)
                                       : tv::decode_partitioned_slots<__bf16>(head_dim, gt);
@@ -291,10 +305,11 @@ int paged_decode_impl(const char* who, void* out, const void* queries, const voi
                        pair ? 1 : 0, sched);
   }
   const dim3 grid(max_parts, num_kv_heads * p.head_chunks, num_seqs);
+  const bool wide = !ordered && decode_wide(num_seqs, num_kv_heads * p.head_chunks, width, partition_size);
   bool launched = false;
-  if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, pair, grid, s);
-  else if (dtype == TV_F16) launched = tv::launch_paged_decode<_Float16>(p, head_dim, gt, pair, grid, s);
-  else launched = tv::launch_paged_decode<__bf16>(p, head_dim, gt, pair, grid, s);
+  if (dtype == TV_F32) launched = tv::launch_paged_decode<float>(p, head_dim, gt, pair, wide, grid, s);
+  else if (dtype == TV_F16) launched = tv::launch_paged_decode<_Float16>(p, head_dim, gt, pair, wide, grid, s);
+  else launched = tv::launch_paged_decode<__bf16>(p, head_dim, gt, pair, wide, grid, s);
   if (!launched) return fail(TV_EUNSUPPORTED, "%s: no kernel for head_dim=%d gt=%d", who, head_dim, gt);
   int rc = check_launch(who);
   if (rc != TV_OK || max_parts <= 1) return rc;
