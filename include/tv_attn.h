@@ -128,7 +128,12 @@ int tv_paged_decode_noalloc(void* out, const void* queries, const void* k_cache,
  * chunk_tiles: key tiles (of 64) per work unit; long causal rows are split into
  * chunks processed by separate work-groups and merged by a second kernel, which
  * needs `workspace` of tv_flash_prefill_workspace_bytes(...) bytes (0 = no
- * split).  chunk_tiles <= 0 picks a size from the shape.
+ * split).  chunk_tiles <= 0 picks a size from the shape: no chunks, except
+ * causal head_dim-128 prompts of 2048+ rows whose 128-row query tiles leave at
+ * least a quarter of the current device's resident work-group slots free
+ * (few heads, e.g. a head-sharded model): their longer tiles run as two key
+ * halves merged by a second kernel (the size then depends on the device).
+ * The workspace must be 16-byte aligned.
  */
 size_t tv_flash_prefill_workspace_bytes(int q_len, int kv_len, int num_heads, int head_dim, int head_dim_v,
                                         int causal, int dtype, int chunk_tiles);

@@ -139,6 +139,53 @@ def test_long_prompts_head_dim_128(dtype, causal, lq, lk, scale):
     check(q.to(dtype), k.to(dtype), v.to(dtype), causal)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out_dtype", [None, torch.float32])
+def test_split_key_halves_workspace_and_fp32_output(dtype, out_dtype):
+    """A causal L 2100 prompt at Hq 8 (17 query tiles of 128 rows, all resident
+    at once) runs tiles 8-16 as two key halves each, merged by a second kernel
+    (flash_prefill_rows.hip): the workspace is sized for the halves, and the
+    merged rows match the oracle in the input type and in fp32."""
+    from tinyvllm_amd import _lib
+    lib = _lib.load()
+    lq = 2100
+    assert lib.tv_flash_prefill_workspace_bytes(lq, lq, 8, 128, 128, 1, _lib.dtype_code(dtype), 0) > 0
+    assert lib.tv_flash_prefill_workspace_bytes(lq, lq, 8, 128, 128, 0, _lib.dtype_code(dtype), 0) == 0
+    q = randn(96, lq, 8, 128).to(dtype)
+    k = randn(97, lq, 2, 128).to(dtype)
+    v = randn(98, lq, 2, 128).to(dtype)
+    out = _op()(q.unsqueeze(0).cuda(), k.unsqueeze(0).cuda(), v.unsqueeze(0).cuda(), True, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert out.dtype == (dtype if out_dtype is None else out_dtype)
+    want = flash_prefill_ref(q.float().numpy()[None], k.float().numpy()[None], v.float().numpy()[None], True)[0]
+    err = np.abs(out[0].float().cpu().numpy() - want).max()
+    assert err <= TOL[dtype], err
+
+
+def test_split_key_halves_replay_in_graph():
+    """The split launch (halves + merge) captured in a HIP graph: replays, with
+    eager work between them, equal the eager launch bit for bit."""
+    from tinyvllm_amd.attention import PrefillPlan
+    q, k, v = (randn(99 + i, 2048, h, 128, dtype=torch.float16).cuda().unsqueeze(0) for i, h in enumerate((8, 2, 2)))
+    plan = PrefillPlan(q, k, v)
+    assert plan.ws_bytes > 0
+    eager = plan.run().clone()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            plan.run()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        plan.out.zero_()
+        junk = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(plan.out, eager)
+        del junk
+
+
 def _check_heads(out, q, k, v, causal, groups, dtype):
     """Oracle rows of the query heads of the listed KV groups only (the float64
     oracle over every head of a large grid would take minutes)."""

@@ -1,5 +1,5 @@
-"""Index arithmetic of the paged prefill kernel, checked on the CPU with the
-kernel's own code.
+"""Index arithmetic of the prefill kernels, checked on the CPU with the
+kernels' own code.
 
 `prefill_fa_kernel<..., PAGED = true>` (tinyvllm_amd/csrc/flash_prefill.hip)
 stages the block ids of a work-group's key range in LDS and maps every key a
@@ -10,7 +10,8 @@ compiles those functions for the host (hipcc, no GPU code) and checks every
 slot for the shapes the GPU tests and the bench launch, for every kernel shape
 (1 / 2 / 4 key groups, 32- / 64-key tiles).  A former clamp (to the last key of
 the sequence instead of the last staged key) is planted through the driver and
-must be caught.
+must be caught.  The same driver checks the 128-row kernel's split causal
+grids: units -> (query tile, key half) and the halves' key ranges.
 """
 
 import shutil
@@ -57,3 +58,15 @@ def test_every_touched_key_maps_to_a_staged_slot(checker, q_len, start, bs, caus
 def test_the_old_clamp_reads_past_the_staged_table(checker):
     res = run(checker, 77, 300, 16, True, planted=True)
     assert res.returncode == 1 and "slot" in res.stdout, res.stdout + res.stderr
+
+
+def test_split_units_cover_every_query_tile_once(checker):
+    """The 128-row kernel's split grids (tinyvllm_amd/csrc/flash_prefill_rows.hip):
+    every tile count up to 64 (L 8192) and every first split tile."""
+    res = subprocess.run([str(checker), "split", "64"], capture_output=True, text=True)
+    assert res.returncode == 0 and res.stdout.startswith("ok "), res.stdout + res.stderr
+
+
+def test_overlapping_key_halves_are_caught(checker):
+    res = subprocess.run([str(checker), "split", "8", "planted"], capture_output=True, text=True)
+    assert res.returncode == 1 and "halves" in res.stdout, res.stdout + res.stderr

@@ -654,11 +654,20 @@ bool prefill_uses_mfma(const PrefillParams& p, int dtype) {
          (p.head_dim == 64 || p.head_dim == 128) && aligned && small_stride;
 }
 
+// 128-row work-groups with LDS-DMA tiles (prefill_rows_kernel,
+// flash_prefill_rows.hip) for long head_dim-128 prompts, where they measured
+// faster (MI355X, Hq 32 / Hkv 8: L 2048 54-56 against 64-68 us, L 4096
+// 174 against 207-210); below 2048 rows, or at head_dim 64, this file's 64-row
+// kernel wins.
+constexpr int kRowsMinLen = 2048;
+
+bool use_rows_kernel(int head_dim, long long max_q_len) { return head_dim == 128 && max_q_len >= kRowsMinLen; }
+
 size_t prefill_workspace_bytes(const PrefillParams& p, int dtype) {
   if (!prefill_uses_mfma(p, dtype)) return 0;
   int units, max_chunks;
   prefill_units(p, units, max_chunks);
-  if (max_chunks <= 1) return 0;
+  if (max_chunks <= 1) return use_rows_kernel(p.head_dim, p.q_len) ? prefill_rows_workspace_bytes(p, dtype) : 0;
   const size_t nqt = (p.q_len + kPrefillBM - 1) / kPrefillBM;
   return (size_t)p.num_heads * nqt * max_chunks * kPrefillBM * (p.head_dim + 2) * sizeof(float);
 }
@@ -686,14 +695,6 @@ void launch_fa(int cfg, dim3 grid, const PrefillParams& pp, hipStream_t stream) 
   else hipLaunchKernelGGL((prefill_fa_kernel<T, D, 1, 1, BN, PAGED>), grid, dim3(256), 0, stream, pp);
 }
 
-// 128-row work-groups with LDS-DMA tiles (prefill_rows_kernel,
-// flash_prefill_rows.hip) for long head_dim-128 prompts, where they measured
-// faster (MI355X, Hq 32 / Hkv 8: L 2048 54-56 against 64-68 us, L 4096
-// 174 against 207-210); below 2048 rows, or at head_dim 64, this file's 64-row
-// kernel wins.
-constexpr int kRowsMinLen = 2048;
-
-bool use_rows_kernel(int head_dim, long long max_q_len) { return head_dim == 128 && max_q_len >= kRowsMinLen; }
 
 // Returns 0 on launch, 1 if the shape has no kernel, 2 if the workspace is missing.
 int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, size_t workspace_bytes,
@@ -704,9 +705,11 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     int units, max_chunks;
     prefill_units(pp, units, max_chunks);
     pp.max_chunks = max_chunks;
-    if (max_chunks == 1 && use_rows_kernel(pp.head_dim, pp.q_len) &&
-        launch_prefill_rows(pp, dtype, 1, pp.q_len, stream))
-      return 0;
+    if (max_chunks == 1 && use_rows_kernel(pp.head_dim, pp.q_len)) {
+      const size_t need = prefill_rows_workspace_bytes(pp, dtype);
+      if (need && (!workspace || workspace_bytes < need)) return 2;
+      if (launch_prefill_rows(pp, dtype, 1, pp.q_len, need ? workspace : nullptr, stream)) return 0;
+    }
     if (max_chunks > 1) {
       const size_t need = prefill_workspace_bytes(pp, dtype);
       if (!workspace || workspace_bytes < need) return 2;
@@ -799,7 +802,7 @@ int launch_flash_prefill_varlen(const PrefillParams& p_in, int num_seqs, int max
   pp.part_o = nullptr;
   pp.part_ml = nullptr;
   if (use_rows_kernel(pp.head_dim, max_q_len) &&
-      launch_prefill_rows(pp, dtype, num_seqs, max_q_len, stream))
+      launch_prefill_rows(pp, dtype, num_seqs, max_q_len, nullptr, stream))
     return 0;
   const int nqt = (max_q_len + kPrefillBM - 1) / kPrefillBM;
   const dim3 grid(pp.num_heads, nqt, num_seqs);

@@ -76,6 +76,7 @@
 #include "tv_common.h"
 #include "tv_params.h"
 #include "tv_device_cache.h"
+#include "tv_paged_keys.h"
 #include "tv_tile_dma.h"
 
 #include <type_traits>
@@ -102,6 +103,12 @@ __device__ __forceinline__ int rows_unit_tile(int u, int nqt, bool longest_first
   if (longest_first) return nqt - 1 - u;
   const int half = (nqt + 1) / 2;
   return u < half ? nqt - 1 - u : u - half;
+}
+
+// Split halves are stored as fp32 unless the input and the output are fp16.
+template <typename T>
+__host__ __device__ constexpr bool rows_split_f32(int out_dtype) {
+  return out_dtype == kF32 || !std::is_same_v<T, _Float16>;
 }
 
 template <typename T, int D>
@@ -140,11 +147,14 @@ prefill_rows_kernel(const PrefillParams pa) {
 
   const int h = p.xcd_remap ? ((int)(blockIdx.x & 7) * (p.num_heads >> 3) + (int)(blockIdx.x >> 3)) : (int)blockIdx.x;
   const int nqt = (p.q_len + BM - 1) / BM;
-  const int qt = rows_unit_tile(blockIdx.y, nqt, p.longest_first != 0);
+  int qt, half = -1;       // half: -1 the tile's whole key range, 0 / 1 its first / second half
+  if (p.rows_split < nqt) rows_split_unit(blockIdx.y, nqt, p.rows_split, qt, half);
+  else qt = rows_unit_tile(blockIdx.y, nqt, p.longest_first != 0);
   const int kvh = h / (p.num_heads / p.num_kv_heads);
   const int klim = p.kv_len;
-  const int kend = p.causal ? min(klim, (qt + 1) * BM) : klim;
-  const int ntiles = (kend + BN - 1) / BN;
+  int kbeg, kend;          // this unit's keys
+  rows_unit_keys(qt, half, p.causal ? min(klim, (qt + 1) * BM) : klim, kbeg, kend);
+  const int ntiles = (kend - kbeg + BN - 1) / BN;
   const float c = p.scale * kLog2e;
   const int row0 = qt * BM + wave * 32;    // first query row of this wave
 
@@ -181,17 +191,16 @@ prefill_rows_kernel(const PrefillParams pa) {
     kvoff[i] = (uint32_t)(row * kstr + chunk * 16);
     vvoff[i] = (uint32_t)(row * vstr + chunk * 16);
   }
-  // tile t (clamped to the last tile) into buffer t % NB; the resource's range
-  // ends at the last key row
-  // Tile t's K / V buffer descriptors (base at the tile's first key row,
-  // range ending at the last key row).  Tiles are requested in order t = 0, 1,
-  // 2, ...; each request advances the descriptors by one tile (64-bit adds,
-  // no per-request multiplies on the scalar unit), and from t = ntiles on the
-  // last tile is requested again.
-  unsigned long long ka = reinterpret_cast<unsigned long long>(kbase);
-  unsigned long long va = reinterpret_cast<unsigned long long>(vbase);
-  unsigned long long kr = (unsigned long long)(klim - 1) * kstr + D * sizeof(T);
-  unsigned long long vr = (unsigned long long)(klim - 1) * vstr + D * sizeof(T);
+  // Tile t (keys kbeg + 32 t ..) into buffer t % NB.  Its K / V buffer
+  // descriptors: base at the tile's first key row, range ending at the last
+  // key row.  Tiles are requested in order t = 0, 1, 2, ...; each request
+  // advances the descriptors by one tile (64-bit adds, no per-request
+  // multiplies on the scalar unit), and from t = ntiles on the last tile is
+  // requested again.
+  unsigned long long ka = reinterpret_cast<unsigned long long>(kbase) + (unsigned long long)kbeg * kstr;
+  unsigned long long va = reinterpret_cast<unsigned long long>(vbase) + (unsigned long long)kbeg * vstr;
+  unsigned long long kr = (unsigned long long)(klim - 1 - kbeg) * kstr + D * sizeof(T);
+  unsigned long long vr = (unsigned long long)(klim - 1 - kbeg) * vstr + D * sizeof(T);
   const unsigned long long kstep = (unsigned long long)BN * kstr;
   const unsigned long long vstep = (unsigned long long)BN * vstr;
   auto issue = [&](int t) {
@@ -264,10 +273,10 @@ prefill_rows_kernel(const PrefillParams pa) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) st[r][kb][i] = fmaf(st[r][kb][i], c, -mref[r]);
     }
-    if (!(k0 + 16 * NKB <= klim && (!p.causal || k0 + 16 * NKB - 1 <= row0))) {
+    if (!(k0 + 16 * NKB <= kend && (!p.causal || k0 + 16 * NKB - 1 <= row0))) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        const int rel = (p.causal ? min(klim - 1, qi[r]) : klim - 1) - (k0 + 4 * g);
+        const int rel = (p.causal ? min(kend - 1, qi[r]) : kend - 1) - (k0 + 4 * g);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -323,7 +332,7 @@ prefill_rows_kernel(const PrefillParams pa) {
     lds_barrier();
     issue(jj + 2);
     issue(jj + 3);
-    const int k0 = jj * BN;
+    const int k0 = kbeg + jj * BN;
     if (idle || (p.causal && k0 > row0 + 31)) return;
     f32x4 st[RB][2 * KB];
 #pragma unroll
@@ -374,21 +383,92 @@ prefill_rows_kernel(const PrefillParams pa) {
   }
   wait_vmcnt<0>();               // the clamped trailing loads land before the work-group ends
 
+  // Normalised rows to out; a split tile's halves to split_o instead (rows of
+  // a half contiguous, fp32 unless both input and output are fp16: one
+  // rounding of a bf16 half plus the output's would double the output's
+  // rounding error), with their (max, sum) -- the log2-domain reference
+  // maximum and the row sum relative to it -- for the merge.
+  const size_t sunit = half >= 0 ? (size_t)h * (nqt - p.rows_split) + (qt - p.rows_split) : 0;
+  void* const obase = half >= 0 ? p.split_o : p.out;
+  const bool f32rows = half >= 0 ? rows_split_f32<T>(p.out_dtype) : p.out_dtype == kF32;
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
     const float lsum = sum_over_g(lpart[r]);
     if (qi[r] >= p.q_len) continue;
     const float inv = 1.0f / lsum;
+    const size_t hrow = (sunit * 2 + (half > 0)) * BM + (qi[r] - qt * BM);   // row of a half
+    if (half >= 0 && g == 0) *reinterpret_cast<float2*>(p.split_ml + hrow * 2) = float2{mref[r], lsum};
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const size_t idx = (size_t)qi[r] * p.out_stride + (size_t)h * D + db * 16 + 4 * g;
+      const size_t idx = (half >= 0 ? hrow * D : (size_t)qi[r] * p.out_stride + (size_t)h * D) + db * 16 + 4 * g;
       const f32x4 v = oacc[r][db] * inv;
-      if (p.out_dtype == kF32) {
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + idx) = v;
+      if (f32rows) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(obase) + idx) = v;
       } else {
         const u32x2 w = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + idx) = w;
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(obase) + idx) = w;
       }
+    }
+  }
+}
+
+// Combines the two key halves of each split query tile: rows (h, qt) of the
+// halves a and b, normalised, with (max, sum) pairs (m_a, l_a), (m_b, l_b)
+// in the log2 domain, become
+//   (w_a O_a + w_b O_b) / (w_a + w_b),  w = l * 2^(m - max(m_a, m_b)),
+// the softmax over the whole key range, written to out.  Grid (Hq,
+// nqt - rows_split), 256 threads; a thread merges 8 elements of a row.  H: the
+// halves' element type, E: the output's.
+template <typename H, typename E, int D>
+__global__ void __launch_bounds__(256) prefill_rows_merge_kernel(const PrefillParams p) {
+  constexpr int BM = kRowsBM;
+  constexpr int PR = D / 8;                 // threads per row
+  constexpr int RP = 256 / PR;              // rows per pass
+  const int h = blockIdx.x, qt = p.rows_split + (int)blockIdx.y;
+  const size_t sunit = (size_t)h * gridDim.y + blockIdx.y;
+  const int piece = threadIdx.x % PR;
+  // 8 elements of type X at x as floats
+  auto load8 = [](const auto* x, float (&f)[8]) {
+    using X = std::remove_cv_t<std::remove_pointer_t<decltype(x)>>;
+    if constexpr (sizeof(X) == 4) {
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(x), hi = *reinterpret_cast<const f32x4*>(x + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[i] = lo[i];
+        f[4 + i] = hi[i];
+      }
+    } else {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(x);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) unpack2<X>(w[i], f[2 * i], f[2 * i + 1]);
+    }
+  };
+  for (int row = threadIdx.x / PR; row < BM; row += RP) {
+    const int qi = qt * BM + row;
+    if (qi >= p.q_len) break;
+    const size_t ra = (sunit * 2) * BM + row, rb = ra + BM;
+    const float2 a = *reinterpret_cast<const float2*>(p.split_ml + ra * 2);
+    const float2 b = *reinterpret_cast<const float2*>(p.split_ml + rb * 2);
+    const float m = fmaxf(a.x, b.x);
+    const float wa = a.y * fast_exp2(a.x - m), wb = b.y * fast_exp2(b.x - m);
+    const float inv = 1.0f / (wa + wb);
+    const float ca = wa * inv, cb = wb * inv;
+    const H* const hs = reinterpret_cast<const H*>(p.split_o);
+    float fa[8], fb[8];
+    load8(hs + ra * D + piece * 8, fa);
+    load8(hs + rb * D + piece * 8, fb);
+    E* const op = reinterpret_cast<E*>(p.out) + (size_t)qi * p.out_stride + (size_t)h * D + piece * 8;
+    if constexpr (sizeof(E) == 4) {
+      *reinterpret_cast<f32x4*>(op) = f32x4{fa[0] * ca + fb[0] * cb, fa[1] * ca + fb[1] * cb,
+                                            fa[2] * ca + fb[2] * cb, fa[3] * ca + fb[3] * cb};
+      *reinterpret_cast<f32x4*>(op + 4) = f32x4{fa[4] * ca + fb[4] * cb, fa[5] * ca + fb[5] * cb,
+                                                fa[6] * ca + fb[6] * cb, fa[7] * ca + fb[7] * cb};
+    } else {
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = pack2<E>(fa[2 * i] * ca + fb[2 * i] * cb, fa[2 * i + 1] * ca + fb[2 * i + 1] * cb);
+      *reinterpret_cast<u32x4*>(op) = w;
     }
   }
 }
@@ -401,24 +481,99 @@ long long rows_resident() {
   return resident_work_groups(slots, prefill_rows_kernel<T, D>, 256);
 }
 
+// First split query tile (rows_split) of a launch; nqt: no split.  One causal
+// prompt with at least as many keys as queries, on a grid that leaves at
+// least a quarter of the resident slots empty: there the last tile's chain of
+// 2 nqt key steps sets the time while CUs holding short tiles (or none) idle,
+// and the key halves of the longer half of the tiles spread that chain over
+// more work-groups.  On a full grid the zig-zag already gives every CU the
+// same work, and a CU's two work-groups together step only ~1.3x as fast as
+// one alone (per-work-group clock stamps at L 2048, Hq 32: 2.1-3.0 us per
+// 64-key step side by side, 1.6 alone), so the extra work-groups and the
+// merge cost more than the shorter chain saves.  Measured (MI355X, fp16,
+// head_dim 128, Hkv 8, split against whole tiles): L 2048 Hq 8 / 16 31.2 /
+// 40.5 against 44.3 / 47.4 us, L 4096 Hq 8 58.4 against 82.6, L 3072 Hq 16
+// 60.8 against 69.2, L 6144 Hq 8 95.6 against 124.9, L 4096 Hq 12 (Hkv 4)
+// 72.2 against 86.0; slower where the split grid overflows the resident slots
+// with short rows: L 2048 Hq 24 / 32 50.0 / 66.0 against 47.4 / 54.9, L 2560
+// Hq 24 67.8 against 58.7.
 template <typename T, int D>
-void launch_rows(const PrefillParams& pp_in, int num_seqs, int max_q_len, hipStream_t stream) {
-  const dim3 grid(pp_in.num_heads, (max_q_len + kRowsBM - 1) / kRowsBM, num_seqs);
+int rows_split_from(const PrefillParams& p, int num_seqs) {
+  const int nqt = (p.q_len + kRowsBM - 1) / kRowsBM;
+  if (num_seqs != 1 || p.cu_q || p.kv_table || !p.causal || p.q_pos_offset != 0 || p.kv_len < p.q_len || nqt < 4)
+    return nqt;
+  const long long resident = rows_resident<T, D>(), heads = p.num_heads;
+  const int split = nqt / 2;
+  if (4 * heads * nqt > 3 * resident) return nqt;
+  if (heads * (2 * nqt - split) > resident && nqt < 24) return nqt;
+  return split;
+}
+
+// Workspace bytes of a split launch: both halves' rows (room for fp32 rows
+// whatever the types, so the size depends on the shape only), then their
+// (max, sum) pairs.
+template <typename T, int D>
+size_t rows_split_layout(const PrefillParams& p, int split, size_t& ml_offset) {
+  const int nqt = (p.q_len + kRowsBM - 1) / kRowsBM;
+  const size_t units = (size_t)p.num_heads * (nqt - split);
+  ml_offset = units * 2 * kRowsBM * D * sizeof(float);
+  return split >= nqt ? 0 : ml_offset + units * 2 * kRowsBM * 2 * sizeof(float);
+}
+
+template <typename T, int D>
+size_t rows_workspace(const PrefillParams& p) {
+  size_t ml_offset;
+  return rows_split_layout<T, D>(p, rows_split_from<T, D>(p, 1), ml_offset);
+}
+
+template <typename T, int D>
+void launch_rows(const PrefillParams& pp_in, int num_seqs, int max_q_len, void* workspace, hipStream_t stream) {
   PrefillParams pp = pp_in;
+  const int nqt = (max_q_len + kRowsBM - 1) / kRowsBM;
+  // the merge moves 16-byte pieces of the workspace and of out's rows
+  const bool aligned16 = (uintptr_t)workspace % 16 == 0 && (uintptr_t)pp.out % 16 == 0 && pp.out_stride % 8 == 0;
+  pp.rows_split = workspace && aligned16 ? rows_split_from<T, D>(pp, num_seqs) : nqt;
+  if (pp.rows_split < nqt) {
+    size_t ml_offset;
+    rows_split_layout<T, D>(pp, pp.rows_split, ml_offset);
+    pp.split_o = workspace;
+    pp.split_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml_offset);
+    pp.longest_first = 0;
+    hipLaunchKernelGGL((prefill_rows_kernel<T, D>), dim3(pp.num_heads, 2 * nqt - pp.rows_split), dim3(256), 0,
+                       stream, pp);
+    const dim3 mgrid(pp.num_heads, nqt - pp.rows_split);
+    using H = std::conditional_t<rows_split_f32<T>(ElemTraits<T>::kCode), float, T>;   // halves of a T output
+    if (pp.out_dtype == kF32)
+      hipLaunchKernelGGL((prefill_rows_merge_kernel<float, float, D>), mgrid, dim3(256), 0, stream, pp);
+    else
+      hipLaunchKernelGGL((prefill_rows_merge_kernel<H, T, D>), mgrid, dim3(256), 0, stream, pp);
+    return;
+  }
+  const dim3 grid(pp.num_heads, nqt, num_seqs);
   pp.longest_first = (long long)grid.x * grid.y * grid.z > rows_resident<T, D>() ? 1 : 0;
   hipLaunchKernelGGL((prefill_rows_kernel<T, D>), grid, dim3(256), 0, stream, pp);
 }
 
+// Workspace of a one-prompt launch (0: no split, or a shape not handled here).
+size_t prefill_rows_workspace_bytes(const PrefillParams& pp, int dtype) {
+  if (!(dtype == kF16 || dtype == kBF16) || !(pp.head_dim == 64 || pp.head_dim == 128)) return 0;
+  if (dtype == kF16) return pp.head_dim == 64 ? rows_workspace<_Float16, 64>(pp) : rows_workspace<_Float16, 128>(pp);
+  return pp.head_dim == 64 ? rows_workspace<__bf16, 64>(pp) : rows_workspace<__bf16, 128>(pp);
+}
+
 // Launch for one prompt (grid.z = 1) or several (cu_q set; grid.z = prompts).
-// Returns false when the shape is not handled here.
-bool launch_prefill_rows(const PrefillParams& pp, int dtype, int num_seqs, int max_q_len, hipStream_t stream) {
+// A one-prompt launch given a workspace of prefill_rows_workspace_bytes may
+// split its longer query tiles.  Returns false when the shape is not handled
+// here.
+bool launch_prefill_rows(const PrefillParams& pp, int dtype, int num_seqs, int max_q_len, void* workspace,
+                         hipStream_t stream) {
   if (!(dtype == kF16 || dtype == kBF16) || !(pp.head_dim == 64 || pp.head_dim == 128)) return false;
   if (dtype == kF16) {
-    if (pp.head_dim == 64) launch_rows<_Float16, 64>(pp, num_seqs, max_q_len, stream);
-    else launch_rows<_Float16, 128>(pp, num_seqs, max_q_len, stream);
+    if (pp.head_dim == 64) launch_rows<_Float16, 64>(pp, num_seqs, max_q_len, workspace, stream);
+    else launch_rows<_Float16, 128>(pp, num_seqs, max_q_len, workspace, stream);
   } else {
-    if (pp.head_dim == 64) launch_rows<__bf16, 64>(pp, num_seqs, max_q_len, stream);
-    else launch_rows<__bf16, 128>(pp, num_seqs, max_q_len, stream);
+    if (pp.head_dim == 64) launch_rows<__bf16, 64>(pp, num_seqs, max_q_len, workspace, stream);
+    else launch_rows<__bf16, 128>(pp, num_seqs, max_q_len, workspace, stream);
   }
   return true;
 }

@@ -384,6 +384,7 @@ int tv_flash_prefill(void* out, const void* q, const void* k, const void* v, int
     return fail(TV_EINVAL, "tv_flash_prefill: token stride smaller than a token row");
   if (q_len > 65535 * 64 || num_heads > 65535)
     return fail(TV_EINVAL, "tv_flash_prefill: grid too large");
+  if ((uintptr_t)workspace % 16 != 0) return fail(TV_EINVAL, "tv_flash_prefill: workspace must be 16-byte aligned");
   tv::PrefillParams p;
   prefill_params(p, out, q, k, v, q_len, kv_len, num_heads, num_kv_heads, head_dim, head_dim_v, q_stride, k_stride,
                  v_stride, out_stride, causal, scale, out_dtype, chunk_tiles);

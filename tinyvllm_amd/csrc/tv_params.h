@@ -49,6 +49,14 @@ struct PrefillParams {
   // 128-row kernel: 1 deals query tiles longest first (grids with more
   // work-groups than are resident at once), 0 zig-zag (prefill_rows_kernel).
   int longest_first;
+  // 128-row kernel, one causal prompt: query tiles rows_split .. nqt - 1 run
+  // as two work-groups over the two halves of their keys (rows_split_unit,
+  // tv_paged_keys.h); both halves' normalised rows go to split_o, their
+  // (max, sum) to split_ml, and prefill_rows_merge_kernel combines them into
+  // out.  rows_split >= nqt: no split.
+  int rows_split;
+  void* split_o;         // [Hq, nqt - rows_split, 2 halves, 128, head_dim], fp32 or fp16
+  float* split_ml;       // [Hq, nqt - rows_split, 2 halves, 128, 2]
 };
 
 // Cache write from a slot mapping or a base slot (kv_cache.hip).
@@ -84,7 +92,9 @@ bool prefill_uses_mfma(const PrefillParams& p, int dtype);
 size_t prefill_workspace_bytes(const PrefillParams& p, int dtype);
 int launch_flash_prefill(const PrefillParams& p, int dtype, void* workspace, size_t workspace_bytes,
                          hipStream_t stream);
-bool launch_prefill_rows(const PrefillParams& p, int dtype, int num_seqs, int max_q_len, hipStream_t stream);
+size_t prefill_rows_workspace_bytes(const PrefillParams& p, int dtype);
+bool launch_prefill_rows(const PrefillParams& p, int dtype, int num_seqs, int max_q_len, void* workspace,
+                         hipStream_t stream);
 int launch_flash_prefill_paged(const PrefillParams& p, int dtype, hipStream_t stream);
 int launch_flash_prefill_varlen(const PrefillParams& p, int num_seqs, int max_q_len, int max_kv_len,
                                 long long total_q, int dtype, hipStream_t stream);
