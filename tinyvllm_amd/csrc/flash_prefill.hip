@@ -106,10 +106,15 @@ __device__ __forceinline__ void store4(void* base, size_t idx, f32x4 v, int out_
 // and brings the scores into the log2 domain relative to m, the running
 // reference maximum of the query (for fp16 inside the matrix cores, with Q
 // pre-scaled and the accumulator initialised to -m; for bf16 with one fp32 fma
-// per score, see kPreScaleQ), so they go straight into v_exp_f32.  m is raised only when a tile exceeds it by more than 8, which
-// after the first tile is rare.  V is staged row-major in LDS and read as
-// the V^T operand with ds_read_b64_tr_b16; the softmax row sums come from one
-// extra MFMA of P against a register of ones.  Tiles are double-buffered in LDS
+// per score, see kPreScaleQ), so they go straight into v_exp_f32.  m is
+// raised only when a tile exceeds it by more than 8, which after the first
+// tile is rare.  V is staged row-major in LDS and read as the V^T operand with
+// ds_read_b64_tr_b16; the softmax row sums come from one extra MFMA of P
+// against a register of ones.  (Row sums by v_dot2 on the VALU instead, as
+// the 128-row kernel does, measured 2-8% slower here: TinyLlama heads L 512 /
+// 1024 7.97 / 13.5 against 8.13 / 13.8 us, both in one launch 15.1 against
+// 15.7, a 512-row chunk over 3584 cached tokens 30.7 against 31.4 -- the matrix
+// pipe has room, the VALU path of a step does not.)  Tiles are double-buffered in LDS
 // and loaded two steps ahead through buffer loads whose range ends at the last
 // key row (rows past kv_len read as zero), one barrier per step.
 

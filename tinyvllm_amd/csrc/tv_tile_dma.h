@@ -51,16 +51,4 @@ __device__ __forceinline__ u32x4 rsrc_words(const void* base, unsigned long long
   return u32x4{sgpr((uint32_t)a), sgpr((uint32_t)(a >> 32)), n, 0x00020000u};
 }
 
-// Two 16-bit ones packed in a word, for row sums by v_dot2.
-template <typename T> inline constexpr uint32_t kOnesPair = 0;
-template <> inline constexpr uint32_t kOnesPair<_Float16> = 0x3C003C00u;
-template <> inline constexpr uint32_t kOnesPair<__bf16> = 0x3F803F80u;
-
-// acc + the sum of the eight packed 16-bit values of p (fp32 accumulation)
-template <typename T> __device__ __forceinline__ float rowsum8(u32x4 p, float acc) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) acc = dot2<T>(p[w], kOnesPair<T>, acc);
-  return acc;
-}
-
 }  // namespace tv
