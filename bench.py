@@ -56,6 +56,37 @@ LONG_TRAFFIC_SOURCE = "profiles/paged_decode_long_bf16_b16.md"
 STEP_TRAFFIC_BYTES = 4220932722
 STEP_TRAFFIC_SOURCE = "profiles/decode_step_tinyllama_b64.md"
 
+# MFMA counters per prefill launch, from one rocprofv3 --pmc pass over
+# `bench.py --prefill-only` (SQ_VALU_MFMA_BUSY_CYCLES summed over the 1024
+# SIMDs, SQ_INSTS_VALU_MFMA_MOPS_F16 in units of 512 FLOPs), recorded in
+# profiles/prefill_tinyllama_f16.md.  Both depend only on the shape (the
+# matrix instructions a launch issues), so this run's own time per launch
+# turns them into a utilisation: busy cycles / 1024 SIMDs / (ms x 2.4 GHz, the
+# clock of the 2.5 PF/s fp16 peak).
+PREFILL_MFMA_COUNTERS = {
+    "L512": (1327104, 2654208),
+    "L1024": (5013504, 10027008),
+    "one_launch": (6340608, 12681216),
+    "llama3_8b_heads_f16_L2048": (34603008, 69206016),
+    "llama3_8b_heads_f16_L4096": (136314880, 272629760),
+    "llama3_8b_heads_f16_L8192": (541065216, 1082130432),
+    "chunk_over_cached_prefix": (17842176, 35684352),
+    "llama3_8b_tp4_shard_f16_L4096": (34078720, 68157440),
+}
+PREFILL_COUNTER_SOURCE = "profiles/prefill_tinyllama_f16.md"
+MFMA_SIMDS = 1024
+PEAK_CLOCK_GHZ = 2.4
+
+
+def mfma_fields(key, ms, flops):
+    """Counter-sourced MFMA utilisation of one prefill launch of ``ms`` ms and
+    ``flops`` algorithmic FLOPs."""
+    busy, mops = PREFILL_MFMA_COUNTERS[key]
+    return {"mfma_busy": round(busy / MFMA_SIMDS / (ms * 1e-3 * PEAK_CLOCK_GHZ * 1e9), 4),
+            "mfma_busy_cycles": busy,
+            "executed_over_algorithmic_flops": round(mops * 512 / flops, 4),
+            "counter_source": PREFILL_COUNTER_SOURCE}
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
@@ -334,8 +365,27 @@ def bench_prefill(steps, warmup):
         long_prompts[f"llama3_8b_heads_f16_L{L8}"] = {
             "value": round(flops8 / (ms8 * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "ms": round(ms8, 5), "flops": flops8,
-            "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)}
+            "frac_of_fp16_mfma_peak": round(flops8 / (ms8 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+            **mfma_fields(f"llama3_8b_heads_f16_L{L8}", ms8, flops8)}
         del q8, k8, v8
+    # The same heads sharded over four GPUs (8 query / 2 KV heads each), one
+    # prompt of 4096 tokens: a grid that leaves most resident slots empty,
+    # where the longer causal query tiles run as two key halves and a second
+    # kernel merges them.
+    g = torch.Generator(device="cuda").manual_seed(0)
+    hqs, hkvs, ds, Ls = 8, 2, 128, 4096
+    qs = torch.randn((1, Ls, hqs, ds), generator=g, device="cuda").half()
+    ks = torch.randn((1, Ls, hkvs, ds), generator=g, device="cuda").half()
+    vs = torch.randn((1, Ls, hkvs, ds), generator=g, device="cuda").half()
+    plan_s = PrefillPlan(qs, ks, vs, True)
+    mss = timed(plan_s.run, steps, warmup, graph=True)
+    flopss = 2 * hqs * ds * Ls * (Ls + 1)
+    long_prompts["llama3_8b_tp4_shard_f16_L4096"] = {
+        "value": round(flopss / (mss * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms": round(mss, 5), "flops": flopss,
+        "frac_of_fp16_mfma_peak": round(flopss / (mss * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+        "split_key_halves": plan_s.ws_bytes > 0,
+        **mfma_fields("llama3_8b_tp4_shard_f16_L4096", mss, flopss)}
+    del qs, ks, vs, plan_s
     chunk = bench_chunk_over_prefix(steps, warmup)
     return wl, {
         "workload": "prefill_tinyllama_f16_L512+L1024 (Hq32 Hkv4 D64, causal) + fused KV write",
@@ -343,8 +393,16 @@ def bench_prefill(steps, warmup):
         "ms_per_prompt": [round(x, 5) for x in per],
         "flops": flops,
         "frac_of_fp16_mfma_peak": round(flops / (tot * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+        "mfma_busy_per_prompt": [mfma_fields(k, ms, 4 * wl.num_heads * wl.head_dim * (n * (n + 1) // 2))["mfma_busy"]
+                                 for k, ms, n in zip(("L512", "L1024"), per, wl.lengths)],
+        "mfma_busy": round(sum(PREFILL_MFMA_COUNTERS[k][0] for k in ("L512", "L1024")) / MFMA_SIMDS
+                           / (tot * 1e-3 * PEAK_CLOCK_GHZ * 1e9), 4),
+        "executed_over_algorithmic_flops": round(
+            sum(PREFILL_MFMA_COUNTERS[k][1] for k in ("L512", "L1024")) * 512 / flops, 4),
+        "counter_source": PREFILL_COUNTER_SOURCE,
         "one_launch": {"value": round(flops / (ms_packed * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
-                       "ms": round(ms_packed, 5), "note": "both prompts in one tv_flash_prefill_varlen launch"},
+                       "ms": round(ms_packed, 5), "note": "both prompts in one tv_flash_prefill_varlen launch",
+                       **mfma_fields("one_launch", ms_packed, flops)},
         "kv_write_ms": round(wms, 5),
         "kv_write_gbs": round(wl.kv_write_bytes() / (wms * 1e-3) / 1e9, 1),
         **long_prompts,
@@ -443,6 +501,8 @@ def bench_chunk_over_prefix(steps, warmup, prefix=3584, chunk=512):
     flops = 4 * hq * d * (chunk * prefix + chunk * (chunk + 1) // 2)
     return {"workload": f"chunk of {chunk} after {prefix} cached tokens, Hq32 Hkv4 D64 fp16, block 16 shuffled",
             "value": round(flops / (ms_new * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms": round(ms_new, 5),
+            "frac_of_fp16_mfma_peak": round(flops / (ms_new * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+            **mfma_fields("chunk_over_cached_prefix", ms_new, flops),
             "per_row_decode_ms": round(ms_old, 5), "speedup": round(ms_old / ms_new, 2),
             "max_abs_diff_vs_per_row": round(float((new.float() - out[:, 0].float()).abs().max()), 6)}
 

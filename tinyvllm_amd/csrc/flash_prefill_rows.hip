@@ -417,13 +417,17 @@ prefill_rows_kernel(const PrefillParams pa) {
 // in the log2 domain, become
 //   (w_a O_a + w_b O_b) / (w_a + w_b),  w = l * 2^(m - max(m_a, m_b)),
 // the softmax over the whole key range, written to out.  Grid (Hq,
-// nqt - rows_split), 256 threads; a thread merges 8 elements of a row.  H: the
+// nqt - rows_split, kRowsMergeParts), 256 threads: work-group z merges rows
+// z BM / kRowsMergeParts .. of the tile, a thread 8 elements of a row.  H: the
 // halves' element type, E: the output's.
+constexpr int kRowsMergeParts = 4;
+
 template <typename H, typename E, int D>
 __global__ void __launch_bounds__(256) prefill_rows_merge_kernel(const PrefillParams p) {
   constexpr int BM = kRowsBM;
   constexpr int PR = D / 8;                 // threads per row
   constexpr int RP = 256 / PR;              // rows per pass
+  constexpr int RZ = BM / kRowsMergeParts;  // rows per work-group
   const int h = blockIdx.x, qt = p.rows_split + (int)blockIdx.y;
   const size_t sunit = (size_t)h * gridDim.y + blockIdx.y;
   const int piece = threadIdx.x % PR;
@@ -443,7 +447,7 @@ __global__ void __launch_bounds__(256) prefill_rows_merge_kernel(const PrefillPa
       for (int i = 0; i < 4; ++i) unpack2<X>(w[i], f[2 * i], f[2 * i + 1]);
     }
   };
-  for (int row = threadIdx.x / PR; row < BM; row += RP) {
+  for (int row = (int)blockIdx.z * RZ + threadIdx.x / PR; row < ((int)blockIdx.z + 1) * RZ; row += RP) {
     const int qi = qt * BM + row;
     if (qi >= p.q_len) break;
     const size_t ra = (sunit * 2) * BM + row, rb = ra + BM;
@@ -541,7 +545,7 @@ void launch_rows(const PrefillParams& pp_in, int num_seqs, int max_q_len, void* 
     pp.longest_first = 0;
     hipLaunchKernelGGL((prefill_rows_kernel<T, D>), dim3(pp.num_heads, 2 * nqt - pp.rows_split), dim3(256), 0,
                        stream, pp);
-    const dim3 mgrid(pp.num_heads, nqt - pp.rows_split);
+    const dim3 mgrid(pp.num_heads, nqt - pp.rows_split, kRowsMergeParts);
     using H = std::conditional_t<rows_split_f32<T>(ElemTraits<T>::kCode), float, T>;   // halves of a T output
     if (pp.out_dtype == kF32)
       hipLaunchKernelGGL((prefill_rows_merge_kernel<float, float, D>), mgrid, dim3(256), 0, stream, pp);
