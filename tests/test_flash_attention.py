@@ -341,6 +341,42 @@ def test_random_shapes(i, hq, hkv, d, lq, lk, causal, dtype, chunk):
     assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]
 
 
+def _random_split_cases(n=None, seed=83):
+    n = case_count(6) if n is None else n
+    rng = np.random.Generator(np.random.PCG64(case_seed(seed)))
+    cases = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4]))
+        hq = hkv * int(rng.choice([2, 4, 8]))
+        hq = min(hq, 16)
+        lq = int(rng.integers(2048, 3300 if hq <= 8 else 2560))   # grids that leave resident slots free
+        lk = lq if rng.random() < 0.6 else lq + int(rng.integers(1, 500))
+        dtype = [torch.float16, torch.bfloat16][int(rng.integers(0, 2))]
+        out_f32 = bool(rng.random() < 0.3)
+        scale = 3.0 if rng.random() < 0.3 else 1.0
+        cases.append((i, hq, hkv, lq, lk, dtype, out_f32, scale))
+    return cases
+
+
+@pytest.mark.parametrize("i,hq,hkv,lq,lk,dtype,out_f32,scale", _random_split_cases())
+def test_random_split_key_halves(i, hq, hkv, lq, lk, dtype, out_f32, scale):
+    """Seeded random causal prompts of 2048+ rows at head_dim 128 with few heads
+    (1-16 query heads over 1-4 KV heads), so the 128-row kernel runs the longer
+    query tiles as two key halves and merges them: Lk >= Lq, fp16 / bf16,
+    outputs in the input type or fp32, and peaked scores; rows of the first and
+    last KV groups' query heads against the oracle."""
+    from tinyvllm_amd import _lib
+    lib = _lib.load()
+    assert lib.tv_flash_prefill_workspace_bytes(lq, lk, hq, 128, 128, 1, _lib.dtype_code(dtype), 0) > 0
+    q = (randn(600 + i, lq, hq, 128) * scale).to(dtype)
+    k = (randn(700 + i, lk, hkv, 128) * scale).to(dtype)
+    v = randn(800 + i, lk, hkv, 128).to(dtype)
+    out = _op()(q.unsqueeze(0).cuda(), k.unsqueeze(0).cuda(), v.unsqueeze(0).cuda(), True,
+                out_dtype=torch.float32 if out_f32 else None)[0]
+    torch.cuda.synchronize()
+    _check_heads(out, q, k, v, True, sorted({0, hkv - 1}), dtype)
+
+
 # ---- several prompts per launch (no reference counterpart) ------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
