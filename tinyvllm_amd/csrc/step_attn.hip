@@ -32,6 +32,14 @@ template <int NT, typename E> __device__ __forceinline__ u32x4 ld_tile(const E* 
   else return *reinterpret_cast<const u32x4*>(p);
 }
 
+// A zero the compiler cannot prove uniform: a load indexed by it stays a
+// vector load, waited for by vmcnt in order with the other vector loads.
+__device__ __forceinline__ int lane_zero() {
+  int z;
+  __asm__ volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 template <typename T, int D, int NW, int PF>
 __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams p) {
   constexpr int KS = D / 32;        // MFMA k steps over the head dim
@@ -150,6 +158,13 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   float2 pv0[SB];
   load_parts(n0, 0, pv0);
   const float2 cs0 = *reinterpret_cast<const float2*>(p.rope + ((size_t)pr * (D / 2) + d2_0) * 2);
+  // The block of the step's token, for its cache slot: a vector load issued
+  // before the tile loads and waited for only where k / v are stored.  (A
+  // scalar load after the tile loads returned ~4 us after the position,
+  // behind the tile stream, by per-work-group clock stamps of a timing copy;
+  // the launch itself is ~0.1 us shorter this way, TinyLlama step at B64.)
+  const int slot_blk = bt[(pos >= 0 ? min(pos / bs, p.bt_stride - 1) : 0) + lane_zero()];
+  __builtin_amdgcn_sched_barrier(0);   // issued here, ahead of the tile loads
 
   // The first tiles' K / V loads depend only on the block table: issue them
   // before the prologue's arithmetic so their latency overlaps it (tile 0 of
@@ -159,11 +174,8 @@ __global__ void __launch_bounds__(64 * NW) step_attn_kernel(const StepAttnParams
   for (int i = 0; i < PF; ++i) load(min(i, max(nt, 1) - 1), 0, t[i]);
 
   // ---- q, k, v of the new token: sums, RoPE, stores --------------------------
-  long long slot = -1;
-  if (pos >= 0 && pos / bs < p.bt_stride) {
-    const int blk = bt[pos / bs];
-    if (blk >= 0 && blk < p.num_blocks) slot = (long long)blk * bs + pos % bs;
-  }
+  const long long slot = pos >= 0 && pos / bs < p.bt_stride && slot_blk >= 0 && slot_blk < p.num_blocks
+                            ? (long long)slot_blk * bs + pos % bs : -1;
   {
     auto finish_item = [&](int it, int d2, float v0, float v1, float2 cs) {
       if (it < nq + D / 2) {
