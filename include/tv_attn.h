@@ -132,7 +132,8 @@ int tv_paged_decode_noalloc(void* out, const void* queries, const void* k_cache,
  * causal head_dim-128 prompts of 2048+ rows whose 128-row query tiles leave at
  * least a quarter of the current device's resident work-group slots free
  * (few heads, e.g. a head-sharded model): their longer tiles run as two key
- * halves merged by a second kernel (the size then depends on the device).
+ * halves merged by a second kernel (the size then depends on the device);
+ * that split is optional -- with workspace NULL such a prompt runs unsplit.
  * The workspace must be 16-byte aligned.
  */
 size_t tv_flash_prefill_workspace_bytes(int q_len, int kv_len, int num_heads, int head_dim, int head_dim_v,

@@ -186,6 +186,30 @@ def test_split_key_halves_replay_in_graph():
         del junk
 
 
+def test_split_shape_without_workspace_runs_unsplit():
+    """A prompt that would split its key halves, given no workspace through the
+    C ABI, runs unsplit and still matches the oracle; a workspace smaller than
+    tv_flash_prefill_workspace_bytes asks for is rejected."""
+    import math
+    from tinyvllm_amd import _lib
+    lib = _lib.load()
+    lq, hq, hkv, d = 2048, 8, 2, 128
+    q, k, v = (randn(110 + i, lq, h, d, dtype=torch.float16) for i, h in enumerate((hq, hkv, hkv)))
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    need = lib.tv_flash_prefill_workspace_bytes(lq, lq, hq, d, d, 1, _lib.TV_F16, 0)
+    assert need > 0
+    out = torch.empty((lq, hq, d), dtype=torch.float16, device="cuda")
+    stream = _lib.stream_ptr(torch.device("cuda"))
+    args = (out.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), lq, lq, hq, hkv, d, d, hq * d, hkv * d,
+            hkv * d, hq * d, 1, 1.0 / math.sqrt(d), _lib.TV_F16, _lib.TV_F16, 0)
+    assert lib.tv_flash_prefill(*args, None, 0, stream) == 0
+    torch.cuda.synchronize()
+    _check_heads(out, q, k, v, True, [0, hkv - 1], torch.float16)
+    small = torch.empty(256, dtype=torch.uint8, device="cuda")
+    assert lib.tv_flash_prefill(*args, small.data_ptr(), 256, stream) == _lib.TV_EINVAL
+    assert b"workspace" in lib.tv_last_error()
+
+
 def _check_heads(out, q, k, v, causal, groups, dtype):
     """Oracle rows of the query heads of the listed KV groups only (the float64
     oracle over every head of a large grid would take minutes)."""

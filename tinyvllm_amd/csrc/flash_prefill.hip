@@ -711,8 +711,10 @@ int launch_flash_prefill(const PrefillParams& p_in, int dtype, void* workspace, 
     prefill_units(pp, units, max_chunks);
     pp.max_chunks = max_chunks;
     if (max_chunks == 1 && use_rows_kernel(pp.head_dim, pp.q_len)) {
+      // the key-half split needs the workspace; without one the prompt runs
+      // unsplit (a workspace smaller than asked for is the caller's error)
       const size_t need = prefill_rows_workspace_bytes(pp, dtype);
-      if (need && (!workspace || workspace_bytes < need)) return 2;
+      if (need && workspace && workspace_bytes < need) return 2;
       if (launch_prefill_rows(pp, dtype, 1, pp.q_len, need ? workspace : nullptr, stream)) return 0;
     }
     if (max_chunks > 1) {
