@@ -90,6 +90,9 @@ def test_validation_errors_are_reported_without_launch():
     rc = lib.tv_flash_prefill(fake, fake, fake, fake, 0, 4, 8, 8, 64, 64, 512, 512, 512, 512,
                               1, 0.1, 1, 1, 0, None, 0, None)
     assert rc == _lib.TV_EINVAL and b"empty" in lib.tv_last_error()
+    rc = lib.tv_flash_prefill(fake, fake, fake, fake, 2048, 2048, 8, 2, 128, 128, 1024, 256, 256, 1024,
+                              1, 0.1, 1, 1, 0, ctypes.c_void_p(24), 1 << 20, None)
+    assert rc == _lib.TV_EINVAL and b"16-byte aligned" in lib.tv_last_error()
     rc = lib.tv_read_kv_blocks(fake, fake, fake, fake, fake, 1, 17, 4, 64, 16, 10, 1, None)
     assert rc == _lib.TV_EINVAL and b"exceeds" in lib.tv_last_error()
 
