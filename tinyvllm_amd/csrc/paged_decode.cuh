@@ -123,6 +123,13 @@ inline bool decode_uniform_tiles(int block_size, int partition_size, int num_kv_
          (long long)TT * num_kv_heads * D * (long long)sizeof(T) < (1LL << 31);
 }
 
+// VGPRs per lane of two tiles in flight (K and V rows), the accumulators and
+// the query vectors of the decode kernel's shape: the part of its register
+// budget that grows when a second tile is requested ahead.
+template <typename T, int D, int GT>
+constexpr int kDecodePipeRegs = 2 * (2 * DecodeShape<T, D, GT>::NR * DecodeShape<T, D, GT>::VPL * 4) +
+                                GT * DecodeShape<T, D, GT>::EPL + GT * DecodeShape<T, D, GT>::VPL * 4;
+
 // Running maxima are only raised when a tile's maximum exceeds them by more
 // than this many log2 units, so most tiles skip the rescale of l and acc; the
 // unnormalised weights stay <= 2^kRescaleSlack, far from fp32 overflow.
@@ -239,8 +246,30 @@ __device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D
   const float sc = p.scale * kLog2e;
   const float bi2 = bias * kLog2e;
 
-  // Fetch the K/V rows of the tile starting at token t0 (rows past `end` or in
-  // an invalid block are zero and marked invalid).
+  // Uniform tiles (UB): the K/V rows of the tile starting at token t0, which
+  // lies in cache block blk (rows past `end` or in an invalid block are zero
+  // and marked invalid; with live false the tile has no rows and consumes as
+  // nothing).
+  auto fetch_block = [&](int t0, int blk, u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR],
+                         bool live) {
+    const bool blk_ok = (unsigned)blk < (unsigned)p.num_blocks;
+    bad |= live && !blk_ok;
+    const int rows = blk_ok && live ? min(TT, end - t0) : 0;
+    const size_t row0 = (size_t)(blk_ok ? blk : 0) * p.block_size + (t0 & (p.block_size - 1));
+    const unsigned long long nrec = (unsigned long long)rows * row_stride * sizeof(T);
+    const auto kres = make_rsrc(kc + row0 * row_stride, nrec);
+    const auto vres = make_rsrc(vc + row0 * row_stride, nrec);
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+      valid[j] = j * RPI + r < rows;
+      const int off = lane_off + j * RPI * (int)(row_stride * sizeof(T));
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        kr[j][v] = buffer_load_nt16(kres, off + v * LPR * 16, 0);
+        vr[j][v] = buffer_load_nt16(vres, off + v * LPR * 16, 0);
+      }
+    }
+  };
   auto fetch = [&](int t0, u32x4 (&kr)[NR][VPL], u32x4 (&vr)[NR][VPL], bool (&valid)[NR]) {
     if constexpr (UB) {
       // The whole tile lies in one cache block: one wave-uniform table lookup,
@@ -248,24 +277,7 @@ __device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D
       // at the last attended row of the tile (nothing when the block id is
       // invalid), so rows past it read as zero without per-row branches, and
       // the lane offsets are the same for every tile.
-      const int blk = bt[t0 >> p.bs_log2];
-      const bool blk_ok = (unsigned)blk < (unsigned)p.num_blocks;
-      bad |= !blk_ok;
-      const int rows = blk_ok ? min(TT, end - t0) : 0;
-      const size_t row0 = (size_t)(blk_ok ? blk : 0) * p.block_size + (t0 & (p.block_size - 1));
-      const unsigned long long nrec = (unsigned long long)rows * row_stride * sizeof(T);
-      const auto kres = make_rsrc(kc + row0 * row_stride, nrec);
-      const auto vres = make_rsrc(vc + row0 * row_stride, nrec);
-#pragma unroll
-      for (int j = 0; j < NR; ++j) {
-        valid[j] = j * RPI + r < rows;
-        const int off = lane_off + j * RPI * (int)(row_stride * sizeof(T));
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) {
-          kr[j][v] = buffer_load_nt16(kres, off + v * LPR * 16, 0);
-          vr[j][v] = buffer_load_nt16(vres, off + v * LPR * 16, 0);
-        }
-      }
+      fetch_block(t0, bt[t0 >> p.bs_log2], kr, vr, valid, true);
     } else {
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
@@ -386,11 +398,37 @@ __device__ __forceinline__ void decode_range(const DecodeParams& p, DecodeSmem<D
     }
   };
 
-  for (int t0 = start + wi * TT; t0 < end; t0 += wph * TT) {
-    u32x4 kr[NR][VPL], vr[NR][VPL];
-    bool valid[NR];
-    fetch(t0, kr, vr, valid);
-    consume(kr, vr, valid);
+  // 8-wave work-groups (small launches, where dependent round trips set the
+  // time) whose waves have at most two tiles: both tiles' block ids are
+  // requested together and both tiles' rows before either is consumed (one
+  // round trip for the table and one for the rows instead of two each; the
+  // second tile of a one-tile wave is a dead re-read of the first).  Only
+  // shapes whose two tiles in flight fit beside the accumulators (no spills
+  // at 256 VGPRs, checked in the compiled code).
+  const int first = start + wi * TT, stride = wph * TT;
+  bool done = false;
+  if constexpr (NW >= 8 && UB && kDecodePipeRegs<T, D, GT> <= 192) {
+    const int n = first < end ? (end - first + stride - 1) / stride : 0;
+    if (n == 1 || n == 2) {
+      const int t1 = first + (n - 1) * stride;
+      const int blk0 = bt[first >> p.bs_log2];
+      const int blk1 = bt[t1 >> p.bs_log2];
+      u32x4 kr0[NR][VPL], vr0[NR][VPL], kr1[NR][VPL], vr1[NR][VPL];
+      bool valid0[NR], valid1[NR];
+      fetch_block(first, blk0, kr0, vr0, valid0, true);
+      fetch_block(t1, blk1, kr1, vr1, valid1, n == 2);
+      consume(kr0, vr0, valid0);
+      consume(kr1, vr1, valid1);
+      done = true;
+    }
+  }
+  if (!done) {
+    for (int t0 = first; t0 < end; t0 += stride) {
+      u32x4 kr[NR][VPL], vr[NR][VPL];
+      bool valid[NR];
+      fetch(t0, kr, vr, valid);
+      consume(kr, vr, valid);
+    }
   }
 
   // ---- merge row groups and waves ------------------------------------------

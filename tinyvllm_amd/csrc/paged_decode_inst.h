@@ -14,7 +14,9 @@ constexpr int kDecodeWaves = 4;   // waves per work-group
 // most kDecodeWideTokens): one unsplit launch of 8-wave work-groups, so a
 // pair's tiles are spread over twice the waves (at most four 16-token tiles
 // each) and no merge launch follows; the waves merge through LDS (64 GT D
-// bytes).  Eight waves cap a wave at 256 VGPRs: the shapes with a wide form,
+// bytes).  The launcher also halves GQA chunks of 4+ heads when the doubled
+// grid still fits the CUs (tv_api.hip), and waves with at most two tiles
+// request both before consuming either (decode_range).  Eight waves cap a wave at 256 VGPRs: the shapes with a wide form,
 // head_dim 64 or 128 with GQA chunks of 2+ heads, fit it without spills in all
 // three element types (others -- head_dim 256, fp32 head_dim 32 with 8 heads,
 // single heads of fp32 head_dim 128 -- would spill); sixteen waves (128 VGPRs)
