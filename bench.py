@@ -605,6 +605,8 @@ def main():
                     help="run only the causal prefill + K/V write workload and print its result (profiling)")
     ap.add_argument("--decode-long-only", action="store_true",
                     help="run only the split-context decode B16 x 32768 and print its result (profiling)")
+    ap.add_argument("--decode-small-only", action="store_true",
+                    help="run only the TinyLlama fp32 B4 paged decode and print its result (profiling)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (HBM counter calibration)")
     ap.add_argument("--read-ceiling-only", action="store_true",
@@ -622,7 +624,8 @@ def main():
     torch.cuda.set_device(0)
     cpu_on = not args.no_cpu_baseline
     env = cpu_env() if cpu_on else None
-    if args.e2e_only or args.prefill_only or args.decode_long_only or args.read_ceiling_only:
+    if (args.e2e_only or args.prefill_only or args.decode_long_only or args.read_ceiling_only
+            or args.decode_small_only):
         if args.calib_copy_mib:
             calibration_copy(args.calib_copy_mib)
         if args.read_ceiling_only:
@@ -631,6 +634,9 @@ def main():
             out = bench_e2e(decode_steps=args.e2e_steps)[1]
         elif args.prefill_only:
             out = bench_prefill(args.steps, args.warmup)[1]
+        elif args.decode_small_only:
+            r1 = bench_decode(workloads.decode_tinyllama_f32_b4(), args.steps, args.warmup, graph=True)
+            out = {"value": round(r1["ms"] * 1e3, 3), "unit": "us", "gbs": round(r1["gbs"], 1), "bytes": r1["bytes"]}
         else:
             out = config_decode_long(args, None, False)
         print(json.dumps(out), flush=True)
