@@ -279,6 +279,20 @@ def test_rejects_bad_arguments():
                torch.from_numpy(cl).to(dev), 8, 4, 64, 16)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 4, 64), (32, 8, 128), (16, 4, 64), (8, 4, 128), (12, 2, 64)])
+def test_small_launch_wide_work_groups(dtype, hq, hkv, d):
+    """Small batches with contexts of at most 512 tokens take one launch of
+    8-wave work-groups: GQA groups of 8 / 4 / 6 / 2 heads (groups of 4+ are
+    served in chunks of half the heads), waves with one or two 16-token tiles
+    (both requested before either is consumed), a partial last block, and a
+    zero-length context."""
+    ctx = [17, 64, 250, 512, 1, 0]
+    case = build_case(2100 + hq + d, [max(c, 1) for c in ctx], hq, hkv, d, 16, dtype)
+    q, kc, vc, bt, _ = case
+    check((q, kc, vc, bt, np.asarray(ctx, np.int32)), hq, hkv, d, 16, dtype)
+
+
 # ---- seeded random shapes -------------------------------------------------------------
 
 def _random_decode_cases(n=None, seed=81):
