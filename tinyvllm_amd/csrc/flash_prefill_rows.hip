@@ -4,7 +4,9 @@
 // Same semantics as prefill_fa_kernel (flash_prefill.hip; reference
 // tinyvllm/model/llama.py:58-94): scores (q.k)*scale, key j excluded for query
 // i when j > i with `causal` (top-left aligned), query head h on KV head
-// h / (Hq/Hkv), fp16 / bf16 inputs, fp32 accumulation, head_dim 64 or 128.
+// h / (Hq/Hkv), fp16 / bf16 inputs, fp32 accumulation.  Launched for head_dim
+// 128 (the kernel body is written for any head_dim whose tile fills the DMA
+// shape; at 64 the 64-row kernel was faster at every length measured).
 //
 // Why a second kernel.  In the 64-row kernel every wave owns 16 query rows, so
 // each K / V byte read from LDS feeds 16 rows of MFMA work: at full matrix
@@ -560,25 +562,20 @@ void launch_rows(const PrefillParams& pp_in, int num_seqs, int max_q_len, void* 
 
 // Workspace of a one-prompt launch (0: no split, or a shape not handled here).
 size_t prefill_rows_workspace_bytes(const PrefillParams& pp, int dtype) {
-  if (!(dtype == kF16 || dtype == kBF16) || !(pp.head_dim == 64 || pp.head_dim == 128)) return 0;
-  if (dtype == kF16) return pp.head_dim == 64 ? rows_workspace<_Float16, 64>(pp) : rows_workspace<_Float16, 128>(pp);
-  return pp.head_dim == 64 ? rows_workspace<__bf16, 64>(pp) : rows_workspace<__bf16, 128>(pp);
+  if (!(dtype == kF16 || dtype == kBF16) || pp.head_dim != 128) return 0;
+  return dtype == kF16 ? rows_workspace<_Float16, 128>(pp) : rows_workspace<__bf16, 128>(pp);
 }
 
 // Launch for one prompt (grid.z = 1) or several (cu_q set; grid.z = prompts).
 // A one-prompt launch given a workspace of prefill_rows_workspace_bytes may
 // split its longer query tiles.  Returns false when the shape is not handled
-// here.
+// here (only head_dim 128 is: at head_dim 64 the 64-row kernel of
+// flash_prefill.hip is faster at every length measured).
 bool launch_prefill_rows(const PrefillParams& pp, int dtype, int num_seqs, int max_q_len, void* workspace,
                          hipStream_t stream) {
-  if (!(dtype == kF16 || dtype == kBF16) || !(pp.head_dim == 64 || pp.head_dim == 128)) return false;
-  if (dtype == kF16) {
-    if (pp.head_dim == 64) launch_rows<_Float16, 64>(pp, num_seqs, max_q_len, workspace, stream);
-    else launch_rows<_Float16, 128>(pp, num_seqs, max_q_len, workspace, stream);
-  } else {
-    if (pp.head_dim == 64) launch_rows<__bf16, 64>(pp, num_seqs, max_q_len, workspace, stream);
-    else launch_rows<__bf16, 128>(pp, num_seqs, max_q_len, workspace, stream);
-  }
+  if (!(dtype == kF16 || dtype == kBF16) || pp.head_dim != 128) return false;
+  if (dtype == kF16) launch_rows<_Float16, 128>(pp, num_seqs, max_q_len, workspace, stream);
+  else launch_rows<__bf16, 128>(pp, num_seqs, max_q_len, workspace, stream);
   return true;
 }
 
