@@ -1,4 +1,5 @@
-"""Paged decode at the benchmark's full sizes (tinyvllm/model/llama.py:97-144).
+"""Paged decode and causal prefill at the benchmark's full sizes
+(tinyvllm/model/llama.py:97-144, 58-94).
 
 The two HBM-bound decode workloads run exactly as bench.py builds and launches
 them: the Llama-3-8B head shape (B256, Hq32 Hkv8 D128, fp16 cache, context
@@ -8,14 +9,19 @@ float64 oracle runs on sampled sequences, whose blocks are gathered from the
 device into a compact cache; the whole batch is checked through properties that
 do not depend on size: repeated launches are bit-identical, and the split and
 unsplit launches agree (the log-sum-exp merge is exact in real arithmetic, so
-they differ by rounding only).  Tolerance: 2e-2 max-abs for fp16/bf16.
+they differ by rounding only).  Prefill at the benchmark's long prompts
+(Llama-3-8B heads at L 4096 / 8192, and the 4-way head shard whose longer
+query tiles run as key halves plus a merge) is checked on sampled query rows:
+row i of a causal prefill is the softmax attention of q_i over keys 0 .. i, so
+the oracle runs on that one row with all heads.  Tolerance: 2e-2 max-abs for
+fp16/bf16.
 """
 
 import numpy as np
 import pytest
 import torch
 
-from oracle.attention import paged_decode_ref
+from oracle.attention import flash_prefill_ref, paged_decode_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -78,4 +84,40 @@ def test_long_bf16_b16_full_size():
         assert torch.isfinite(out).all()
     finally:
         del wl
+        torch.cuda.empty_cache()
+
+
+def _prefill_rows_check(L, hq, hkv, dtype, seed):
+    """Bench-shaped causal prefill (inputs drawn as bench.py draws its long
+    prompts); sampled rows against the float64 oracle, a repeat bit-identical."""
+    from tinyvllm_amd.attention import flash_prefill_attention
+    d = 128
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn((1, L, hq, d), generator=g, device="cuda").to(dtype)
+    k = torch.randn((1, L, hkv, d), generator=g, device="cuda").to(dtype)
+    v = torch.randn((1, L, hkv, d), generator=g, device="cuda").to(dtype)
+    out = flash_prefill_attention(q, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    rng = np.random.Generator(np.random.PCG64(seed + 1))
+    # first rows, both sides of 128-row tile and key-half boundaries, the last rows, random rows
+    rows = sorted({0, 1, 127, 128, 2047, 2048, L // 2 + 63, L // 2 + 64, L - 2, L - 1,
+                   *rng.choice(L, 6, replace=False).tolist()})
+    qh, kh, vh = q[0].float().cpu().numpy(), k[0].float().cpu().numpy(), v[0].float().cpu().numpy()
+    got = out[0].float().cpu().numpy()
+    for i in rows:
+        want = flash_prefill_ref(qh[None, i:i + 1], kh[None, :i + 1], vh[None, :i + 1], causal=False)[0, 0]
+        err = np.abs(got[i] - want).max()
+        assert err <= TOL, f"L {L} Hq {hq} row {i}: max-abs {err}"
+    again = flash_prefill_attention(q, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(again, out)
+
+
+@pytest.mark.parametrize("L,hq,hkv,dtype", [(4096, 32, 8, torch.float16), (8192, 32, 8, torch.float16),
+                                             (4096, 32, 8, torch.bfloat16), (4096, 8, 2, torch.float16)])
+def test_prefill_long_prompts_full_size(L, hq, hkv, dtype):
+    try:
+        _prefill_rows_check(L, hq, hkv, dtype, seed=0)
+    finally:
         torch.cuda.empty_cache()
