@@ -62,18 +62,6 @@ template <> __device__ __forceinline__ float dot2<__bf16>(uint32_t a, uint32_t b
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-// Two 16-bit ones packed in a word, for row sums by v_dot2.
-template <typename T> inline constexpr uint32_t kOnesPair = 0;
-template <> inline constexpr uint32_t kOnesPair<_Float16> = 0x3C003C00u;
-template <> inline constexpr uint32_t kOnesPair<__bf16> = 0x3F803F80u;
-
-// acc + the sum of the eight packed 16-bit values of p (fp32 accumulation)
-template <typename T> __device__ __forceinline__ float rowsum8(u32x4 p, float acc) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) acc = dot2<T>(p[w], kOnesPair<T>, acc);
-  return acc;
-}
-
 // Round a float to T (round-to-nearest-even) and back to raw bits.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
